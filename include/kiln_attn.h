@@ -1,0 +1,138 @@
+/*
+ * kiln_attn.h - C ABI of the MI355X (gfx950) fused attention path of Kiln's diffusion engine.
+ *
+ * One shared library, kiln_amd/libkiln_attn.so. Every entry point:
+ *   - takes plain device pointers, element strides and sizes (no framework types);
+ *   - enqueues work on the given HIP stream (NULL = the default stream) and never synchronizes;
+ *   - returns a kiln_status (0 = OK); kiln_attn_last_error() gives a detail message for the
+ *     calling thread. The C++ header kiln_amd/host/kiln_gpu.hpp turns non-zero codes into
+ *     std::runtime_error, the reference op layer's error behaviour (engine/src/gpu.h:15-16,
+ *     engine/src/kernels.cu:870).
+ *
+ * Layout contract (the reference's, engine/src/gpu.h:149-153): row-major [T, ld] matrices with the
+ * row stride ld in elements; head h occupies columns [h*Dh, (h+1)*Dh). Rows must be 16-byte
+ * aligned. Keys beyond Tk are never read; npad extra all-zero keys (K = 0, V = 0) are accounted for
+ * analytically (they add npad*exp(-max) to the softmax denominator and nothing to the output).
+ *
+ * fp16 values cross the ABI as uint16_t bit patterns (IEEE binary16), bf16 norm weights likewise.
+ */
+#ifndef KILN_ATTN_H
+#define KILN_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* kiln_stream_t; /* identical to hipStream_t */
+
+typedef enum {
+    KILN_OK = 0,
+    KILN_EINVAL = 1,       /* bad argument (null pointer, negative size, ...) */
+    KILN_EUNSUPPORTED = 2, /* shape/stride/alignment this path does not take (reference: attention16 throws) */
+    KILN_EHIP = 3,         /* a HIP runtime call or kernel launch failed */
+    KILN_ENOMEM = 4        /* workspace allocation failed or the given workspace is too small */
+} kiln_status;
+
+typedef enum { KILN_F32 = 0, KILN_F16 = 1 } kiln_dtype;
+
+const char* kiln_attn_status_string(int status);
+const char* kiln_attn_last_error(void);
+/* gfx target of device `dev` as "gfx950" etc.; returns KILN_EHIP if no device. */
+int kiln_attn_device_arch(int dev, char* buf, int buflen);
+
+/* ------------------------------------------------------------------------------------------
+ * Drop-in replacements of the reference op layer
+ * ------------------------------------------------------------------------------------------ */
+
+/* Replaces attention() (engine/src/gpu.h:149-153, impl engine/src/kernels.cu:828-866).
+ * fp32 Q/K/V/out. Dh == 128 and !causal run the fp16-MFMA flash kernel (the reference's
+ * tfa::k_flash<float> path, engine/src/tcflash.cuh:20-157); any other Dh (<= 256) or causal runs
+ * the exact fp32 kernel (the reference's cuBLAS fallback semantics, kernels.cu:809-866).
+ * Uses a library-owned, grow-only device workspace for the fp16 K/V tiles. */
+int kiln_attn_fwd_f32out(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                         int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream);
+
+/* Replaces attention16() (engine/src/gpu.h:155-156, impl engine/src/kernels.cu:868-873).
+ * fp32 Q/K/V, fp16 out; Dh must be 128 (KILN_EUNSUPPORTED otherwise, where the reference throws). */
+int kiln_attn_fwd_f16out(uint16_t* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                         int ldv, int Tq, int Tk, int H, int Dh, int npad, kiln_stream_t stream);
+
+/* Exact fp32 attention (the reference's fallback when G.fp16 is off: --fp32 / "precision":"fp32",
+ * engine/src/kernels.cu:840-865): any Dh <= 256, optional causal mask, npad. */
+int kiln_attn_fwd_exact(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                        int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream);
+
+/* Replaces the rmsnorm() calls of the DiT QK-norm (engine/src/gpu.h:133, kernels.cu:656-673):
+ * per row of `dim`, y = x * rsqrt(mean(x^2) + eps) * w (w bf16, NULL = 1). In place allowed. */
+int kiln_rmsnorm_rows(float* y, const float* x, const uint16_t* w_bf16, int rows, int dim, float eps,
+                      kiln_stream_t stream);
+
+/* Replaces rope_half() (engine/src/gpu.h:145, kernels.cu:759-777): rotate pairs (i, i+Dh/2) of every
+ * head of x [T, H*Dh] (dense rows) with tables cos/sin [T, Dh/2], in place. */
+int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream);
+
+/* Replaces the k_nag<T><<<T,256>>> launch (engine/src/dit.cu:295-324, launched :486 / :524):
+ * per row of `dim` columns, a <- alpha*clamp(g) + (1-alpha)*a, g = a*s - an*(s-1), the clamp limiting
+ * |g|_1 to tau*|a|_1. dtype KILN_F16 (fp16 rows, fp32 math) or KILN_F32. */
+int kiln_nag_combine(void* a, int lda, const void* an, int ldn, int dtype, int T, int dim, float s, float tau,
+                     float alpha, kiln_stream_t stream);
+
+/* Host-side Cosmos 3D RoPE tables for an Hp x Wp patch grid (engine/src/dit.cu:196-215):
+ * cos_t, sin_t are HOST arrays of Hp*Wp*64 floats. */
+int kiln_cosmos_rope_tables(float* cos_t, float* sin_t, int Hp, int Wp);
+
+/* ------------------------------------------------------------------------------------------
+ * MI355X-native entry points of the same path (no counterpart with this signature in the
+ * reference; they batch what the reference does per batch element, engine/src/dit.cu:466-487)
+ * ------------------------------------------------------------------------------------------ */
+
+/* Bytes of a prepared K/V buffer for Tk keys and H heads of dim 128: K and V in fp16, tiled
+ * 64 keys at a time in the MFMA operand order the attention kernel reads, zero beyond Tk. */
+size_t kiln_kv_prepped_bytes(int Tk, int H);
+
+/* Prepare K/V once (e.g. the cross-attention context K/V cached per generation, the reference's
+ * Dit::cache_context, engine/src/dit.cu:217-234). k, v: [Tk, ld] in_dtype rows, head h at column
+ * h*128. Optional per-head RMSNorm of K (k_norm_w bf16 [128], eps) and RoPE of K (tables [Tk, 64]). */
+int kiln_kv_prepare(uint16_t* kvp, const void* k, int ldk, const void* v, int ldv, int in_dtype, int Tk, int H,
+                    const uint16_t* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                    kiln_stream_t stream);
+
+/* Attention of Q [Tq, ldq] (in_dtype) against a prepared K/V buffer. The Q tile load applies the
+ * optional per-head RMSNorm (q_norm_w, eps) and RoPE (tables [Tq, 64]) before the fp16 rounding. */
+int kiln_attn_fwd_prepped(void* out, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
+                          const uint16_t* q_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                          const uint16_t* kvp, int Tq, int Tk, int H, int npad, kiln_stream_t stream);
+
+/* Plain batched fp16 attention: B independent (Q, K, V) sets at batch strides bs* (elements). */
+int kiln_attn_fwd_f16in(void* out, int out_dtype, int ldo, long long bso, const uint16_t* q, int ldq, long long bsq,
+                        const uint16_t* k, int ldk, long long bsk, const uint16_t* v, int ldv, long long bsv, int B,
+                        int Tq, int Tk, int H, int npad, void* workspace, size_t ws_bytes, kiln_stream_t stream);
+size_t kiln_attn_fwd_f16in_workspace_bytes(int B, int Tk, int H);
+
+/* Fused DiT self-attention of a CFG batch (engine/src/dit.cu:458-470): q, k, v are the raw
+ * projections [B*T, ld] (batch b at rows b*T); QK-RMSNorm (bf16 weights, eps) and RoPE (tables
+ * [T, 64]) are applied inside (K in the K/V prepare pass, Q in the attention kernel's tile load),
+ * softmax scale 1/sqrt(128). out [B*T, ldo] in out_dtype. workspace NULL = library-owned. */
+int kiln_dit_self_attn_fused(void* out, int out_dtype, int ldo, const void* q, const void* k, const void* v,
+                             int in_dtype, int ld, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                             const float* rope_cos, const float* rope_sin, int B, int T, int H, void* workspace,
+                             size_t ws_bytes, kiln_stream_t stream);
+size_t kiln_dit_self_attn_workspace_bytes(int B, int T, int H);
+
+/* DiT cross-attention of a CFG batch plus NAG (engine/src/dit.cu:473-487): batch item b's queries
+ * (rows b*T of q, RMS-normed inside with q_norm_w) attend to prepared context kvp[b] (Lk[b] real keys,
+ * npad[b] zero keys). If kvp_neg is not NULL, item 0's queries also attend to kvp_neg into
+ * out_neg [T, ldo] (caller scratch) and item 0's output is replaced by the NAG combine with
+ * (nag_scale, nag_tau, nag_alpha). B <= 3. */
+int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
+                        const uint16_t* q_norm_w, float eps, int B, int T, int H, const uint16_t* const* kvp,
+                        const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,
+                        float nag_scale, float nag_tau, float nag_alpha, kiln_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KILN_ATTN_H */

@@ -1,0 +1,239 @@
+"""kiln_amd — MI355X (gfx950) fused attention path of Kiln's diffusion engine.
+
+The product is the C-ABI library ``kiln_amd/libkiln_attn.so`` (declared in include/kiln_attn.h).
+This module binds it with ctypes and offers thin torch-tensor wrappers named after the reference
+op layer (engine/src/gpu.h:133-156): ``attention``, ``attention16``, ``rmsnorm``, ``rope_half``,
+``nag_combine`` plus the batched/fused entry points. Tensors must live on the GPU; there is no CPU
+fallback — when the library is missing, ``lib()`` raises.
+
+Errors: a non-zero status from the library raises ``KilnError`` (the reference raises
+std::runtime_error, engine/src/kernels.cu:870).
+"""
+import ctypes
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libkiln_attn.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "kiln_attn.h")
+
+KILN_OK, KILN_EINVAL, KILN_EUNSUPPORTED, KILN_EHIP, KILN_ENOMEM = 0, 1, 2, 3, 4
+KILN_F32, KILN_F16 = 0, 1
+
+_i, _ll, _f, _vp, _sz = ctypes.c_int, ctypes.c_longlong, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+
+# symbol -> (restype, argtypes)
+_SIGS = {
+    "kiln_attn_status_string": (ctypes.c_char_p, [_i]),
+    "kiln_attn_last_error": (ctypes.c_char_p, []),
+    "kiln_attn_device_arch": (_i, [_i, ctypes.c_char_p, _i]),
+    "kiln_attn_fwd_f32out": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "kiln_attn_fwd_f16out": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "kiln_attn_fwd_exact": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "kiln_rmsnorm_rows": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "kiln_rope_half": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "kiln_nag_combine": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _f, _f, _f, _vp]),
+    "kiln_cosmos_rope_tables": (_i, [_vp, _vp, _i, _i]),
+    "kiln_kv_prepped_bytes": (_sz, [_i, _i]),
+    "kiln_kv_prepare": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _f, _vp, _vp, _vp]),
+    "kiln_attn_fwd_prepped": (_i, [_vp, _i, _i, _vp, _i, _i, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "kiln_attn_fwd_f16in": (_i, [_vp, _i, _i, _ll, _vp, _i, _ll, _vp, _i, _ll, _vp, _i, _ll, _i, _i, _i, _i, _i,
+                                 _vp, _sz, _vp]),
+    "kiln_attn_fwd_f16in_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kiln_dit_self_attn_fused": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp,
+                                      _sz, _vp]),
+    "kiln_dit_self_attn_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kiln_cross_attn_nag": (_i, [_vp, _vp, _i, _i, _vp, _i, _i, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _f,
+                                 _f, _f, _vp]),
+}
+
+_LIB = None
+
+
+class KilnError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"kiln status {status}: {msg}")
+        self.status = status
+
+
+def lib():
+    """Load libkiln_attn.so (build it first with ``python -m kiln_amd.build``)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m kiln_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def header_symbols(path=HEADER_PATH):
+    """Function names declared in include/kiln_attn.h."""
+    with open(path) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(kiln_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+def _check(rc):
+    if rc != KILN_OK:
+        msg = lib().kiln_attn_last_error().decode()
+        raise KilnError(rc, msg)
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _dt(t):
+    import torch
+    if t.dtype == torch.float16:
+        return KILN_F16
+    if t.dtype == torch.float32:
+        return KILN_F32
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _bf16_bits(w):
+    """bf16 weight tensor (or None) -> pointer; torch.bfloat16 storage is the bf16 bit pattern."""
+    import torch
+    if w is None:
+        return None
+    if w.dtype != torch.bfloat16 or not w.is_contiguous() or w.numel() < 128:
+        raise TypeError("norm weights must be a contiguous bf16 tensor of >= 128 elements")
+    return _ptr(w)
+
+
+def _ld(t):
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError("expected a 2-D row-major tensor")
+    return t.stride(0)
+
+
+# ---------------------------------------------------------------------------------------------
+# reference-named op layer (engine/src/gpu.h)
+# ---------------------------------------------------------------------------------------------
+def attention(out, q, k, v, Tq, Tk, H, Dh=128, causal=False, npad=0, stream=None):
+    """attention() (engine/src/gpu.h:149-153): fp32 q/k/v/out rows, head h at column h*Dh."""
+    _check(lib().kiln_attn_fwd_f32out(_ptr(out), _ld(out), _ptr(q), _ld(q), _ptr(k), _ld(k), _ptr(v), _ld(v), Tq, Tk,
+                                      H, Dh, int(causal), npad, _stream(stream)))
+    return out
+
+
+def attention16(out, q, k, v, Tq, Tk, H, Dh=128, npad=0, stream=None):
+    """attention16() (engine/src/gpu.h:155-156): fp32 q/k/v, fp16 out."""
+    _check(lib().kiln_attn_fwd_f16out(_ptr(out), _ld(out), _ptr(q), _ld(q), _ptr(k), _ld(k), _ptr(v), _ld(v), Tq, Tk,
+                                      H, Dh, npad, _stream(stream)))
+    return out
+
+
+def attention_exact(out, q, k, v, Tq, Tk, H, Dh, causal=False, npad=0, stream=None):
+    """Exact fp32 attention (the reference's --fp32 fallback semantics)."""
+    _check(lib().kiln_attn_fwd_exact(_ptr(out), _ld(out), _ptr(q), _ld(q), _ptr(k), _ld(k), _ptr(v), _ld(v), Tq, Tk,
+                                     H, Dh, int(causal), npad, _stream(stream)))
+    return out
+
+
+def rmsnorm(y, x, w=None, rows=None, dim=128, eps=1e-6, stream=None):
+    """rmsnorm() over rows of `dim` (engine/src/gpu.h:133); fp32, in place allowed."""
+    rows = x.numel() // dim if rows is None else rows
+    _check(lib().kiln_rmsnorm_rows(_ptr(y), _ptr(x), _bf16_bits(w), rows, dim, eps, _stream(stream)))
+    return y
+
+
+def rope_half(x, T, H, Dh, cos_t, sin_t, stream=None):
+    """rope_half() (engine/src/gpu.h:145): in place on dense fp32 rows [T, H*Dh]."""
+    _check(lib().kiln_rope_half(_ptr(x), T, H, Dh, _ptr(cos_t), _ptr(sin_t), _stream(stream)))
+    return x
+
+
+def nag_combine(a, an, scale=5.0, tau=2.5, alpha=0.25, stream=None):
+    """k_nag (engine/src/dit.cu:295-324): a <- NAG(a, an) in place, rows of a.shape[1]."""
+    _check(lib().kiln_nag_combine(_ptr(a), _ld(a), _ptr(an), _ld(an), _dt(a), a.shape[0], a.shape[1], scale, tau,
+                                  alpha, _stream(stream)))
+    return a
+
+
+def cosmos_rope_tables(Hp, Wp):
+    """Cosmos 3D RoPE cos/sin tables [Hp*Wp, 64] as CPU float32 tensors (engine/src/dit.cu:196-215)."""
+    import torch
+    c = torch.empty(Hp * Wp, 64, dtype=torch.float32)
+    s = torch.empty(Hp * Wp, 64, dtype=torch.float32)
+    _check(lib().kiln_cosmos_rope_tables(_ptr(c), _ptr(s), Hp, Wp))
+    return c, s
+
+
+# ---------------------------------------------------------------------------------------------
+# MI355X-native batched / fused entry points
+# ---------------------------------------------------------------------------------------------
+def kv_prepped_bytes(Tk, H):
+    return lib().kiln_kv_prepped_bytes(Tk, H)
+
+
+def kv_prepare(k, v, H, k_norm_w=None, eps=1e-6, rope=None, stream=None):
+    """Prepare K/V (fp16 tiled MFMA order, optional K RMSNorm/RoPE); returns a uint8 device buffer."""
+    import torch
+    Tk = k.shape[0]
+    buf = torch.empty(max(kv_prepped_bytes(Tk, H), 16), dtype=torch.uint8, device=k.device)
+    rc, rs = rope if rope is not None else (None, None)
+    _check(lib().kiln_kv_prepare(_ptr(buf), _ptr(k), _ld(k), _ptr(v), _ld(v), _dt(k), Tk, H, _bf16_bits(k_norm_w),
+                                 eps, _ptr(rc), _ptr(rs), _stream(stream)))
+    return buf
+
+
+def attn_prepped(out, q, kvp, Tk, H, npad=0, q_norm_w=None, eps=1e-6, rope=None, stream=None):
+    rc, rs = rope if rope is not None else (None, None)
+    _check(lib().kiln_attn_fwd_prepped(_ptr(out), _dt(out), _ld(out), _ptr(q), _dt(q), _ld(q), _bf16_bits(q_norm_w),
+                                       eps, _ptr(rc), _ptr(rs), _ptr(kvp), q.shape[0], Tk, H, npad, _stream(stream)))
+    return out
+
+
+def attn_f16in(out, q, k, v, B, Tq, Tk, H, npad=0, workspace=None, stream=None):
+    """Batched fp16 attention: q/k/v/out are [B*T, ld] with batch b at rows b*T."""
+    ws = _ptr(workspace) if workspace is not None else None
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().kiln_attn_fwd_f16in(_ptr(out), _dt(out), _ld(out), Tq * _ld(out), _ptr(q), _ld(q), Tq * _ld(q),
+                                     _ptr(k), _ld(k), Tk * _ld(k), _ptr(v), _ld(v), Tk * _ld(v), B, Tq, Tk, H, npad,
+                                     ws, wsb, _stream(stream)))
+    return out
+
+
+def dit_self_attn_workspace_bytes(B, T, H):
+    return lib().kiln_dit_self_attn_workspace_bytes(B, T, H)
+
+
+def dit_self_attn(out, q, k, v, B, T, H, q_norm_w, k_norm_w, rope, eps=1e-6, workspace=None, stream=None):
+    """Fused DiT self-attention (QK-RMSNorm + RoPE + attention) of a CFG batch; q/k/v [B*T, ld]."""
+    if not (_ld(q) == _ld(k) == _ld(v)):
+        raise ValueError("q, k, v must share one row stride")
+    ws = _ptr(workspace) if workspace is not None else None
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    rc, rs = rope
+    _check(lib().kiln_dit_self_attn_fused(_ptr(out), _dt(out), _ld(out), _ptr(q), _ptr(k), _ptr(v), _dt(q), _ld(q),
+                                          _bf16_bits(q_norm_w), _bf16_bits(k_norm_w), eps, _ptr(rc), _ptr(rs), B, T,
+                                          H, ws, wsb, _stream(stream)))
+    return out
+
+
+def cross_attn_nag(out, q, B, T, H, kvps, Lks, npads, q_norm_w=None, eps=1e-6, kvp_neg=None, Lk_neg=0, npad_neg=0,
+                   out_neg=None, scale=5.0, tau=2.5, alpha=0.25, stream=None):
+    """DiT cross-attention of a CFG batch with optional NAG on item 0 (engine/src/dit.cu:473-487)."""
+    n = len(kvps)
+    ptrs = (ctypes.c_void_p * n)(*[k.data_ptr() for k in kvps])
+    lks = (ctypes.c_int * n)(*Lks)
+    nps = (ctypes.c_int * n)(*npads)
+    _check(lib().kiln_cross_attn_nag(_ptr(out), _ptr(out_neg), _dt(out), _ld(out), _ptr(q), _dt(q), _ld(q),
+                                     _bf16_bits(q_norm_w), eps, B, T, H, ctypes.cast(ptrs, _vp),
+                                     ctypes.cast(lks, _vp), ctypes.cast(nps, _vp), _ptr(kvp_neg), Lk_neg, npad_neg,
+                                     scale, tau, alpha, _stream(stream)))
+    return out

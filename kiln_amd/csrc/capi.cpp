@@ -1,0 +1,388 @@
+// C ABI of libkiln_attn.so: argument checks, workspace handling and kernel dispatch.
+// Declarations and contracts: include/kiln_attn.h.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/kiln_attn.h"
+#include "common.hpp"
+#include "internal.hpp"
+
+using kiln::DT;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return KILN_OK;
+    return fail(KILN_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Library-owned grow-only device workspace, one per device (used when the caller passes none).
+// Calls are stream-ordered on the caller's stream; concurrent calls on different streams of one
+// device must pass their own workspaces.
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::vector<Workspace> g_ws;
+
+int get_workspace(size_t need, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_check(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
+    Workspace& w = g_ws[dev];
+    if (w.bytes < need) {
+        if (w.ptr) {
+            // earlier stream-ordered users of the old buffer must finish before it is released
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_check(e, "hipDeviceSynchronize");
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        size_t sz = need + need / 4;
+        e = hipMalloc(&w.ptr, sz);
+        if (e != hipSuccess) {
+            w.ptr = nullptr;
+            return fail(KILN_ENOMEM, "workspace hipMalloc(%zu): %s", sz, hipGetErrorString(e));
+        }
+        w.bytes = sz;
+    }
+    *out = w.ptr;
+    return KILN_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// row alignment for 16-byte vector loads of 8-element chunks
+bool rows_ok(const void* p, int ld, DT dt) {
+    if (!aligned16(p)) return false;
+    return dt == DT::F16 ? (ld % 8) == 0 : (ld % 4) == 0;
+}
+
+int check_common(int Tq, int Tk, int H, int npad) {
+    if (Tq < 0 || Tk < 0 || H <= 0 || npad < 0) return fail(KILN_EINVAL, "bad sizes Tq=%d Tk=%d H=%d npad=%d", Tq, Tk, H, npad);
+    if (Tk == 0 && npad == 0 && Tq > 0) return fail(KILN_EINVAL, "no keys (Tk=0, npad=0): softmax undefined");
+    return KILN_OK;
+}
+
+// output when there are no real keys but npad zero keys: softmax mass all on zero values -> 0
+int zero_rows(void* out, int ldo, size_t esz, int Tq, int H, int Dh, hipStream_t s) {
+    hipError_t e = hipMemset2DAsync(out, (size_t)ldo * esz, 0, (size_t)H * Dh * esz, Tq, s);
+    return hip_check(e, "hipMemset2DAsync");
+}
+
+int flash_self(void* out, DT od, int ldo, long long bso, const void* q, int ldq, long long bsq, const void* k, int ldk,
+               long long bsk, const void* v, int ldv, long long bsv, DT in, int B, int Tq, int Tk, int H, int npad,
+               const uint16_t* qw, const uint16_t* kw, float eps, const float* rc, const float* rs, void* ws,
+               size_t ws_bytes, hipStream_t stream) {
+    if (B <= 0 || B > kiln::MAX_JOBS) return fail(KILN_EUNSUPPORTED, "batch %d outside 1..%d", B, kiln::MAX_JOBS);
+    const size_t per = kiln_kv_prepped_bytes(Tk, H);
+    const size_t need = per * B;
+    if (!ws) {
+        int rc2 = get_workspace(need, &ws);
+        if (rc2) return rc2;
+    } else if (ws_bytes < need) {
+        return fail(KILN_ENOMEM, "workspace %zu bytes < %zu needed", ws_bytes, need);
+    }
+    const size_t isz = in == DT::F16 ? 2 : 4, osz = od == DT::F16 ? 2 : 4;
+    kiln::AttnLaunch a{};
+    for (int b = 0; b < B; b++) {
+        uint16_t* kvp = reinterpret_cast<uint16_t*>((char*)ws + per * b);
+        int r = hip_check(kiln::launch_kv_prep(kvp, (const char*)k + bsk * b * isz, ldk, (const char*)v + bsv * b * isz,
+                                               ldv, in, Tk, H, kw, eps, rc, rs, stream),
+                          "kv_prep launch");
+        if (r) return r;
+        a.job[b] = {(const char*)q + bsq * b * isz, kvp, (char*)out + bso * b * osz, Tk, npad};
+    }
+    a.njobs = B;
+    a.Tq = Tq;
+    a.H = H;
+    a.ldq = ldq;
+    a.ldo = ldo;
+    a.in = in;
+    a.out = od;
+    a.qw = qw;
+    a.eps = eps;
+    a.rcos = rc;
+    a.rsin = rs;
+    return hip_check(kiln::launch_attn_fwd(a, stream), "attn_fwd launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kiln_attn_status_string(int status) {
+    switch (status) {
+        case KILN_OK: return "ok";
+        case KILN_EINVAL: return "invalid argument";
+        case KILN_EUNSUPPORTED: return "unsupported shape, stride or alignment";
+        case KILN_EHIP: return "HIP runtime error";
+        case KILN_ENOMEM: return "out of device memory / workspace too small";
+        default: return "unknown status";
+    }
+}
+
+const char* kiln_attn_last_error(void) { return g_err; }
+
+int kiln_attn_device_arch(int dev, char* buf, int buflen) {
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return hip_check(e, "hipGetDeviceProperties");
+    snprintf(buf, buflen, "%s", prop.gcnArchName);
+    return KILN_OK;
+}
+
+size_t kiln_kv_prepped_bytes(int Tk, int H) {
+    if (Tk <= 0 || H <= 0) return 0;
+    return (size_t)H * kiln::kv_head_stride(Tk) * 2;
+}
+
+int kiln_kv_prepare(uint16_t* kvp, const void* k, int ldk, const void* v, int ldv, int in_dtype, int Tk, int H,
+                    const uint16_t* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                    kiln_stream_t stream) {
+    if (in_dtype != KILN_F32 && in_dtype != KILN_F16) return fail(KILN_EINVAL, "in_dtype %d", in_dtype);
+    DT in = (DT)in_dtype;
+    if (Tk < 0 || H <= 0) return fail(KILN_EINVAL, "bad sizes Tk=%d H=%d", Tk, H);
+    if (Tk == 0) return KILN_OK;
+    if (!kvp || !k || !v) return fail(KILN_EINVAL, "null pointer");
+    if (!aligned16(kvp)) return fail(KILN_EUNSUPPORTED, "kvp not 16-byte aligned");
+    if (!rows_ok(k, ldk, in) || !rows_ok(v, ldv, in)) return fail(KILN_EUNSUPPORTED, "K/V rows not 16-byte aligned");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(KILN_EINVAL, "rope tables: need both cos and sin");
+    if (rope_cos && (!aligned16(rope_cos) || !aligned16(rope_sin))) return fail(KILN_EUNSUPPORTED, "rope tables not 16-byte aligned");
+    return hip_check(kiln::launch_kv_prep(kvp, k, ldk, v, ldv, in, Tk, H, k_norm_w, eps, rope_cos, rope_sin,
+                                          (hipStream_t)stream),
+                     "kv_prep launch");
+}
+
+int kiln_attn_fwd_prepped(void* out, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
+                          const uint16_t* q_norm_w, float eps, const float* rope_cos, const float* rope_sin,
+                          const uint16_t* kvp, int Tq, int Tk, int H, int npad, kiln_stream_t stream) {
+    if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
+        return fail(KILN_EINVAL, "dtype");
+    int r = check_common(Tq, Tk, H, npad);
+    if (r) return r;
+    if (Tq == 0) return KILN_OK;
+    if (!out || !q || (Tk > 0 && !kvp)) return fail(KILN_EINVAL, "null pointer");
+    const DT in = (DT)in_dtype, od = (DT)out_dtype;
+    if (Tk == 0) return zero_rows(out, ldo, od == DT::F16 ? 2 : 4, Tq, H, 128, (hipStream_t)stream);
+    if (!rows_ok(q, ldq, in) || !aligned16(kvp)) return fail(KILN_EUNSUPPORTED, "Q rows / kvp not 16-byte aligned");
+    if (ldo % 2) return fail(KILN_EUNSUPPORTED, "ldo must be even");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(KILN_EINVAL, "rope tables: need both cos and sin");
+    kiln::AttnLaunch a{};
+    a.job[0] = {q, kvp, out, Tk, npad};
+    a.njobs = 1;
+    a.Tq = Tq;
+    a.H = H;
+    a.ldq = ldq;
+    a.ldo = ldo;
+    a.in = in;
+    a.out = od;
+    a.qw = q_norm_w;
+    a.eps = eps;
+    a.rcos = rope_cos;
+    a.rsin = rope_sin;
+    return hip_check(kiln::launch_attn_fwd(a, (hipStream_t)stream), "attn_fwd launch");
+}
+
+int kiln_attn_fwd_f32out(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                         int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream) {
+    int r = check_common(Tq, Tk, H, npad);
+    if (r) return r;
+    if (Tq == 0) return KILN_OK;
+    if (!out || !q || (Tk > 0 && (!k || !v))) return fail(KILN_EINVAL, "null pointer");
+    const bool flash = Dh == 128 && !causal && rows_ok(q, ldq, DT::F32) && rows_ok(k, ldk, DT::F32) &&
+                       rows_ok(v, ldv, DT::F32) && ldo % 2 == 0;
+    if (!flash) return kiln_attn_fwd_exact(out, ldo, q, ldq, k, ldk, v, ldv, Tq, Tk, H, Dh, causal, npad, stream);
+    if (Tk == 0) return zero_rows(out, ldo, 4, Tq, H, Dh, (hipStream_t)stream);
+    return flash_self(out, DT::F32, ldo, 0, q, ldq, 0, k, ldk, 0, v, ldv, 0, DT::F32, 1, Tq, Tk, H, npad, nullptr,
+                      nullptr, 0.f, nullptr, nullptr, nullptr, 0, (hipStream_t)stream);
+}
+
+int kiln_attn_fwd_f16out(uint16_t* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                         int ldv, int Tq, int Tk, int H, int Dh, int npad, kiln_stream_t stream) {
+    int r = check_common(Tq, Tk, H, npad);
+    if (r) return r;
+    if (Dh != 128) return fail(KILN_EUNSUPPORTED, "attention16: unsupported head size %d (needs 128)", Dh);
+    if (Tq == 0) return KILN_OK;
+    if (!out || !q || (Tk > 0 && (!k || !v))) return fail(KILN_EINVAL, "null pointer");
+    if (!rows_ok(q, ldq, DT::F32) || !rows_ok(k, ldk, DT::F32) || !rows_ok(v, ldv, DT::F32) || ldo % 2)
+        return fail(KILN_EUNSUPPORTED, "attention16: unsupported row stride or alignment");
+    if (Tk == 0) return zero_rows(out, ldo, 2, Tq, H, Dh, (hipStream_t)stream);
+    return flash_self(out, DT::F16, ldo, 0, q, ldq, 0, k, ldk, 0, v, ldv, 0, DT::F32, 1, Tq, Tk, H, npad, nullptr,
+                      nullptr, 0.f, nullptr, nullptr, nullptr, 0, (hipStream_t)stream);
+}
+
+int kiln_attn_fwd_exact(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                        int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream) {
+    int r = check_common(Tq, Tk, H, npad);
+    if (r) return r;
+    if (Dh <= 0 || Dh > 256) return fail(KILN_EUNSUPPORTED, "exact attention: head size %d outside 1..256", Dh);
+    if (Tq == 0) return KILN_OK;
+    if (!out || !q || (Tk > 0 && (!k || !v))) return fail(KILN_EINVAL, "null pointer");
+    if (Tk == 0) return zero_rows(out, ldo, 4, Tq, H, Dh, (hipStream_t)stream);
+    return hip_check(kiln::launch_exact_attn(out, ldo, q, ldq, k, ldk, v, ldv, Tq, Tk, H, Dh, causal != 0, npad,
+                                             (hipStream_t)stream),
+                     "exact_attn launch");
+}
+
+size_t kiln_attn_fwd_f16in_workspace_bytes(int B, int Tk, int H) {
+    return B > 0 ? (size_t)B * kiln_kv_prepped_bytes(Tk, H) : 0;
+}
+
+int kiln_attn_fwd_f16in(void* out, int out_dtype, int ldo, long long bso, const uint16_t* q, int ldq, long long bsq,
+                        const uint16_t* k, int ldk, long long bsk, const uint16_t* v, int ldv, long long bsv, int B,
+                        int Tq, int Tk, int H, int npad, void* workspace, size_t ws_bytes, kiln_stream_t stream) {
+    if (out_dtype != KILN_F32 && out_dtype != KILN_F16) return fail(KILN_EINVAL, "out_dtype %d", out_dtype);
+    int r = check_common(Tq, Tk, H, npad);
+    if (r) return r;
+    if (B <= 0) return fail(KILN_EINVAL, "B=%d", B);
+    if (Tq == 0) return KILN_OK;
+    if (!out || !q || (Tk > 0 && (!k || !v))) return fail(KILN_EINVAL, "null pointer");
+    const DT od = (DT)out_dtype;
+    if (Tk == 0) {
+        for (int b = 0; b < B; b++) {
+            r = zero_rows((char*)out + bso * b * (od == DT::F16 ? 2 : 4), ldo, od == DT::F16 ? 2 : 4, Tq, H, 128,
+                          (hipStream_t)stream);
+            if (r) return r;
+        }
+        return KILN_OK;
+    }
+    if (!rows_ok(q, ldq, DT::F16) || !rows_ok(k, ldk, DT::F16) || !rows_ok(v, ldv, DT::F16) || ldo % 2 ||
+        bsq % 8 || bsk % 8 || bsv % 8 || bso % 2)
+        return fail(KILN_EUNSUPPORTED, "rows / batch strides not 16-byte aligned");
+    return flash_self(out, od, ldo, bso, q, ldq, bsq, k, ldk, bsk, v, ldv, bsv, DT::F16, B, Tq, Tk, H, npad, nullptr,
+                      nullptr, 0.f, nullptr, nullptr, workspace, ws_bytes, (hipStream_t)stream);
+}
+
+size_t kiln_dit_self_attn_workspace_bytes(int B, int T, int H) {
+    return B > 0 ? (size_t)B * kiln_kv_prepped_bytes(T, H) : 0;
+}
+
+int kiln_dit_self_attn_fused(void* out, int out_dtype, int ldo, const void* q, const void* k, const void* v,
+                             int in_dtype, int ld, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                             const float* rope_cos, const float* rope_sin, int B, int T, int H, void* workspace,
+                             size_t ws_bytes, kiln_stream_t stream) {
+    if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
+        return fail(KILN_EINVAL, "dtype");
+    if (B <= 0 || T <= 0 || H <= 0) return fail(KILN_EINVAL, "bad sizes B=%d T=%d H=%d", B, T, H);
+    if (!out || !q || !k || !v) return fail(KILN_EINVAL, "null pointer");
+    const DT in = (DT)in_dtype, od = (DT)out_dtype;
+    if (!rows_ok(q, ld, in) || !rows_ok(k, ld, in) || !rows_ok(v, ld, in) || ldo % 2)
+        return fail(KILN_EUNSUPPORTED, "rows not 16-byte aligned");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(KILN_EINVAL, "rope tables: need both cos and sin");
+    if (rope_cos && (!aligned16(rope_cos) || !aligned16(rope_sin))) return fail(KILN_EUNSUPPORTED, "rope tables not 16-byte aligned");
+    const long long bs = (long long)T * ld, bso = (long long)T * ldo;
+    return flash_self(out, od, ldo, bso, q, ld, bs, k, ld, bs, v, ld, bs, in, B, T, T, H, 0, q_norm_w, k_norm_w, eps,
+                      rope_cos, rope_sin, workspace, ws_bytes, (hipStream_t)stream);
+}
+
+int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
+                        const uint16_t* q_norm_w, float eps, int B, int T, int H, const uint16_t* const* kvp,
+                        const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,
+                        float nag_scale, float nag_tau, float nag_alpha, kiln_stream_t stream) {
+    if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
+        return fail(KILN_EINVAL, "dtype");
+    const int nj = B + (kvp_neg ? 1 : 0);
+    if (B <= 0 || nj > kiln::MAX_JOBS) return fail(KILN_EUNSUPPORTED, "B=%d (+NAG) outside 1..%d jobs", B, kiln::MAX_JOBS);
+    if (T <= 0 || H <= 0 || !out || !q || !kvp || !Lk || !npad || (kvp_neg && !out_neg))
+        return fail(KILN_EINVAL, "bad sizes or null pointer");
+    const DT in = (DT)in_dtype, od = (DT)out_dtype;
+    if (!rows_ok(q, ldq, in) || ldo % 2) return fail(KILN_EUNSUPPORTED, "Q rows not 16-byte aligned / ldo odd");
+    const size_t isz = in == DT::F16 ? 2 : 4, osz = od == DT::F16 ? 2 : 4;
+    kiln::AttnLaunch a{};
+    int n = 0;
+    for (int b = 0; b < B; b++) {
+        if (Lk[b] <= 0 || npad[b] < 0 || !kvp[b] || !aligned16(kvp[b]))
+            return fail(KILN_EINVAL, "context %d: Lk=%d npad=%d", b, Lk[b], npad[b]);
+        a.job[n++] = {(const char*)q + (size_t)b * T * ldq * isz, kvp[b], (char*)out + (size_t)b * T * ldo * osz, Lk[b],
+                      npad[b]};
+    }
+    if (kvp_neg) {
+        if (Lk_neg <= 0 || npad_neg < 0 || !aligned16(kvp_neg)) return fail(KILN_EINVAL, "NAG context Lk=%d", Lk_neg);
+        a.job[n++] = {q, kvp_neg, out_neg, Lk_neg, npad_neg};
+    }
+    a.njobs = n;
+    a.Tq = T;
+    a.H = H;
+    a.ldq = ldq;
+    a.ldo = ldo;
+    a.in = in;
+    a.out = od;
+    a.qw = q_norm_w;
+    a.eps = eps;
+    int r = hip_check(kiln::launch_attn_fwd(a, (hipStream_t)stream), "attn_fwd launch");
+    if (r || !kvp_neg) return r;
+    return hip_check(kiln::launch_nag(out, ldo, out_neg, ldo, od, T, H * 128, nag_scale, nag_tau, nag_alpha,
+                                      (hipStream_t)stream),
+                     "nag launch");
+}
+
+int kiln_rmsnorm_rows(float* y, const float* x, const uint16_t* w_bf16, int rows, int dim, float eps,
+                      kiln_stream_t stream) {
+    if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes");
+    if (rows && (!y || !x)) return fail(KILN_EINVAL, "null pointer");
+    return hip_check(kiln::launch_rmsnorm_rows(y, x, w_bf16, rows, dim, eps, (hipStream_t)stream), "rmsnorm launch");
+}
+
+int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {
+    if (T < 0 || H <= 0 || Dh <= 0 || Dh % 2) return fail(KILN_EINVAL, "bad sizes");
+    if (T && (!x || !cos_t || !sin_t)) return fail(KILN_EINVAL, "null pointer");
+    return hip_check(kiln::launch_rope_half(x, T, H, Dh, cos_t, sin_t, (hipStream_t)stream), "rope launch");
+}
+
+int kiln_nag_combine(void* a, int lda, const void* an, int ldn, int dtype, int T, int dim, float s, float tau,
+                     float alpha, kiln_stream_t stream) {
+    if (dtype != KILN_F32 && dtype != KILN_F16) return fail(KILN_EINVAL, "dtype %d", dtype);
+    if (T < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes");
+    if (T && (!a || !an)) return fail(KILN_EINVAL, "null pointer");
+    return hip_check(kiln::launch_nag(a, lda, an, ldn, (DT)dtype, T, dim, s, tau, alpha, (hipStream_t)stream),
+                     "nag launch");
+}
+
+// Cosmos 3D RoPE for one image (engine/src/dit.cu:196-215): 22 temporal (identity at T=1), 21 height and
+// 21 width frequencies over the 64 rotated pairs of a 128-dim head; NTK-scaled theta for height/width.
+int kiln_cosmos_rope_tables(float* cos_t, float* sin_t, int Hp, int Wp) {
+    if (!cos_t || !sin_t || Hp <= 0 || Wp <= 0) return fail(KILN_EINVAL, "bad arguments");
+    const int dh = 128 / 6 * 2, dt = 128 - 2 * dh, half = 64;
+    const double ntk = pow(4.0, (double)dh / (dh - 2));
+    const float theta = (float)(10000.0 * ntk);
+    float freq[32];
+    for (int j = 0; j < dh / 2; j++) freq[j] = 1.0f / powf(theta, (float)(2 * j) / (float)dh);
+    for (int y = 0; y < Hp; y++)
+        for (int x = 0; x < Wp; x++) {
+            float* c = cos_t + ((size_t)y * Wp + x) * half;
+            float* s = sin_t + ((size_t)y * Wp + x) * half;
+            for (int i = 0; i < dt / 2; i++) { c[i] = 1.f; s[i] = 0.f; }
+            for (int j = 0; j < dh / 2; j++) {
+                const float ah = (float)y * freq[j], aw = (float)x * freq[j];
+                c[dt / 2 + j] = cosf(ah);
+                s[dt / 2 + j] = sinf(ah);
+                c[dt / 2 + dh / 2 + j] = cosf(aw);
+                s[dt / 2 + dh / 2 + j] = sinf(aw);
+            }
+        }
+    return KILN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Shared device helpers and the kernel-side layout constants of the gfx950 attention path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kiln {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int HD = 128;            // head dim of the flash path
+constexpr int KT = 64;             // keys per K/V tile
+constexpr int TILE_H = KT * HD;    // halves in one K (or V) tile = 16 KB
+constexpr int KV_TILE_H = 2 * TILE_H;  // K tile followed by V tile, 32 KB
+constexpr float LOG2E = 1.4426950408889634f;
+
+// Prepared K/V buffer of one context: [H][ntiles][K tile | V tile], fp16.
+//  K tile order [kb 2][s 8][lane 64][e 8]:  key = kb*32 + lane%32,  d = 16*s + 8*(lane/32) + e
+//    (lane's 16 bytes are exactly the A operand of v_mfma_f32_32x32x16_f16 for S^T = K Q^T)
+//  V tile order [db 4][t 4][lane 64][j 8]:  d = db*32 + lane%32,
+//    key = 16*t + 8*(j/4) + 4*(lane/32) + j%4
+//    (the A operand of O^T = V^T P^T whose B operand P^T is taken straight from the S^T accumulator)
+__host__ __device__ inline int kv_tiles(int Tk) { return (Tk + KT - 1) / KT; }
+__host__ __device__ inline size_t kv_head_stride(int Tk) { return (size_t)kv_tiles(Tk) * KV_TILE_H; }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// 8 consecutive elements of a row as fp32 (fp16 or fp32 storage); p is 16-byte aligned.
+__device__ __forceinline__ void load8(const _Float16* p, float (&x)[8]) {
+    half8 h = *reinterpret_cast<const half8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = (float)h[e];
+}
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+    floatx4 a = *reinterpret_cast<const floatx4*>(p);
+    floatx4 b = *reinterpret_cast<const floatx4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) { x[e] = a[e]; x[e + 4] = b[e]; }
+}
+
+__device__ __forceinline__ half8 to_half8(const float (&x)[8]) {
+    half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (_Float16)x[e];  // RN-even
+    return h;
+}
+
+// lanes l and l^32 exchange: returns (own + partner) for every lane (v_permlane32_swap).
+__device__ __forceinline__ float pair_sum(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_max(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+}  // namespace kiln

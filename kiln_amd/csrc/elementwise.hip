@@ -1,0 +1,174 @@
+// Bandwidth-bound kernels around the attention call: per-head RMSNorm, rotate-half RoPE, NAG combine,
+// and the exact fp32 attention used when the fp16 path does not apply (causal, Dh != 128, fp32 mode).
+#include <math.h>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace kiln {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+// block of 256 threads (4 waves); red must hold 4 floats
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+__device__ __forceinline__ float block_max256(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// ---- RMSNorm over rows of `dim` (engine/src/kernels.cu:656-666): one wave per row ----
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(float* y, const float* x, const uint16_t* w, int rows, int dim,
+                                                      float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * dim;
+    float* yr = y + (size_t)row * dim;
+    float s = 0.f;
+    for (int i = lane; i < dim; i += 64) s += xr[i] * xr[i];
+    const float r = rsqrtf(wave_sum(s) / (float)dim + eps);
+    for (int i = lane; i < dim; i += 64) yr[i] = xr[i] * r * (w ? bf16_to_f32(w[i]) : 1.f);
+}
+
+hipError_t launch_rmsnorm_rows(float* y, const float* x, const uint16_t* w, int rows, int dim, float eps, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3((rows + 3) / 4), dim3(256), 0, s, y, x, w, rows, dim, eps);
+    return hipGetLastError();
+}
+
+// ---- rotate-half RoPE (engine/src/kernels.cu:759-772): one thread per rotated pair ----
+__global__ __launch_bounds__(256) void k_rope_half(float* x, int T, int H, int Dh, const float* ct, const float* st) {
+    const int half = Dh / 2;
+    const size_t n = (size_t)T * H * half;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n) return;
+    const int i = (int)(idx % half);
+    const size_t th = idx / half;
+    const int t = (int)(th / H);
+    float* p = x + th * Dh;
+    const float c = ct[(size_t)t * half + i], sn = st[(size_t)t * half + i];
+    const float a = p[i], b = p[i + half];
+    p[i] = a * c - b * sn;
+    p[i + half] = b * c + a * sn;
+}
+
+hipError_t launch_rope_half(float* x, int T, int H, int Dh, const float* c, const float* sn, hipStream_t s) {
+    const size_t n = (size_t)T * H * (Dh / 2);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_half, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, T, H, Dh, c, sn);
+    return hipGetLastError();
+}
+
+// ---- NAG combine (engine/src/dit.cu:295-324): one block per token row, fp32 arithmetic ----
+__device__ __forceinline__ float ldv(const float* p) { return *p; }
+__device__ __forceinline__ float ldv(const _Float16* p) { return (float)*p; }
+__device__ __forceinline__ void stv(float* p, float v) { *p = v; }
+__device__ __forceinline__ void stv(_Float16* p, float v) { *p = (_Float16)v; }
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_nag(T* a, int lda, const T* an, int ldn, int dim, float s, float tau,
+                                             float alpha) {
+    __shared__ float red[4];
+    T* p = a + (size_t)blockIdx.x * lda;
+    const T* n = an + (size_t)blockIdx.x * ldn;
+    float lp = 0.f, lg = 0.f;
+    for (int i = threadIdx.x; i < dim; i += 256) {
+        const float pi = ldv(p + i);
+        const float g = pi * s - ldv(n + i) * (s - 1.f);
+        lp += fabsf(pi);
+        lg += fabsf(g);
+    }
+    const float tp = block_sum256(lp, red);
+    const float tg = block_sum256(lg, red);
+    const float ratio = tg / fmaxf(tp, 1e-12f);
+    const float k = ratio > tau ? tau / ratio : 1.f;
+    for (int i = threadIdx.x; i < dim; i += 256) {
+        const float pi = ldv(p + i);
+        const float g = pi * s - ldv(n + i) * (s - 1.f);
+        stv(p + i, alpha * g * k + (1.f - alpha) * pi);
+    }
+}
+
+hipError_t launch_nag(void* a, int lda, const void* an, int ldn, DT dt, int T, int dim, float sc, float tau,
+                      float alpha, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    if (dt == DT::F16)
+        hipLaunchKernelGGL(k_nag<_Float16>, dim3(T), dim3(256), 0, s, (_Float16*)a, lda, (const _Float16*)an, ldn, dim,
+                           sc, tau, alpha);
+    else
+        hipLaunchKernelGGL(k_nag<float>, dim3(T), dim3(256), 0, s, (float*)a, lda, (const float*)an, ldn, dim, sc, tau,
+                           alpha);
+    return hipGetLastError();
+}
+
+// ---- exact fp32 attention: one block per (query, head), keys in chunks with an online softmax ----
+// Semantics of the reference's fp32 fallback (engine/src/kernels.cu:809-866): s = (q.k)/sqrt(Dh),
+// causal limit key <= query, with npad the max starts at 0 and npad*exp(-m) joins the denominator.
+constexpr int EX_CH = 256;
+__global__ __launch_bounds__(256) void k_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k,
+                                                    int ldk, const float* v, int ldv, int Tk, int H, int Dh,
+                                                    int causal, int npad, float scale) {
+    __shared__ float qs[256];
+    __shared__ float ps[EX_CH];
+    __shared__ float red[4];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const float* qr = q + (size_t)t * ldq + (size_t)h * Dh;
+    for (int d = tid; d < Dh; d += 256) qs[d] = qr[d];
+    __syncthreads();
+    const int lim = causal ? min(t + 1, Tk) : Tk;
+    float m = npad ? 0.f : -INFINITY, l = 0.f, acc = 0.f;
+    for (int c0 = 0; c0 < lim; c0 += EX_CH) {
+        const int j = c0 + tid;
+        float sj = -INFINITY;
+        if (tid < EX_CH && j < lim) {
+            const float* kr = k + (size_t)j * ldk + (size_t)h * Dh;
+            float a = 0.f;
+            for (int d = 0; d < Dh; d++) a += qs[d] * kr[d];
+            sj = a * scale;
+        }
+        const float cm = block_max256(sj, red);
+        const float mn = fmaxf(m, cm);
+        const float corr = expf(m - mn);
+        m = mn;
+        const float pj = (j < lim) ? expf(sj - m) : 0.f;
+        ps[tid] = pj;
+        const float psum = block_sum256(pj, red);
+        l = l * corr + psum;
+        acc *= corr;
+        __syncthreads();
+        if (tid < Dh) {
+            const int n = min(EX_CH, lim - c0);
+            const float* vr = v + (size_t)c0 * ldv + (size_t)h * Dh + tid;
+            for (int jj = 0; jj < n; jj++) acc += ps[jj] * vr[(size_t)jj * ldv];
+        }
+        __syncthreads();
+    }
+    if (npad) l += (float)npad * expf(-m);
+    if (tid < Dh) out[(size_t)t * ldo + (size_t)h * Dh + tid] = acc / l;
+}
+
+hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                             int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s) {
+    if (Tq <= 0 || H <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_exact_attn, dim3(Tq, H), dim3(256), 0, s, out, ldo, q, ldq, k, ldk, v, ldv, Tk, H, Dh,
+                       causal ? 1 : 0, npad, 1.f / sqrtf((float)Dh));
+    return hipGetLastError();
+}
+
+}  // namespace kiln

@@ -1,0 +1,45 @@
+// Host-side launchers shared between the kernel translation units and the C ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kiln {
+
+enum class DT { F32 = 0, F16 = 1 };
+
+// One attention problem of a batched launch: queries q (rows [0, Tq), row stride ldq, head h at
+// column h*128) against the prepared K/V buffer kv (Tk real keys, npad analytic zero keys).
+struct AttnJob {
+    const void* q;
+    const uint16_t* kv;
+    void* o;
+    int Tk;
+    int npad;
+};
+constexpr int MAX_JOBS = 4;
+
+struct AttnLaunch {
+    AttnJob job[MAX_JOBS];
+    int njobs;
+    int Tq, H, ldq, ldo;
+    DT in, out;
+    const uint16_t* qw;  // bf16 [128] q RMSNorm weight or null (no norm)
+    float eps;
+    const float* rcos;   // [Tq, 64] RoPE tables for Q or null
+    const float* rsin;
+};
+
+hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s);
+
+hipError_t launch_kv_prep(uint16_t* kvp, const void* k, int ldk, const void* v, int ldv, DT in, int Tk, int H,
+                          const uint16_t* kw, float eps, const float* rcos, const float* rsin, hipStream_t s);
+
+hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
+                             int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s);
+
+hipError_t launch_rmsnorm_rows(float* y, const float* x, const uint16_t* w, int rows, int dim, float eps, hipStream_t s);
+hipError_t launch_rope_half(float* x, int T, int H, int Dh, const float* c, const float* sn, hipStream_t s);
+hipError_t launch_nag(void* a, int lda, const void* an, int ldn, DT dt, int T, int dim, float sc, float tau,
+                      float alpha, hipStream_t s);
+
+}  // namespace kiln

@@ -1,0 +1,129 @@
+"""CPU oracle of the fused attention path — TEST INFRASTRUCTURE ONLY.
+
+Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, always as the
+checker (or the timed CPU baseline), never as a product path. numpy in, numpy out.
+See oracle/oracle.c for the reference file:line each function restates and what pins it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i = ctypes.c_int
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            from . import build as _b  # noqa: F401  (oracle/build.py)
+            _b.build()
+        L = ctypes.CDLL(path)
+        L.oracle_ref_attn_f32.argtypes = [_f32p, _i, _f32p, _i, _f32p, _i, _f32p, _i, _i, _i, _i, _i, _i]
+        L.oracle_attn_f64.argtypes = [_f32p, _i, _f32p, _i, _f32p, _i, _f32p, _i, _i, _i, _i, _i, _i, _i,
+                                      ctypes.c_double]
+        L.oracle_attn_f16sem.argtypes = [_f32p, _i, _f32p, _i, _f32p, _i, _f32p, _i, _i, _i, _i, _i, _i]
+        L.oracle_rmsnorm_rows.argtypes = [_f32p, _f32p, ctypes.c_void_p, ctypes.c_long, _i, ctypes.c_float]
+        L.oracle_rope_half.argtypes = [_f32p, _i, _i, _i, _i, _f32p, _f32p]
+        L.oracle_cosmos_rope.argtypes = [_f32p, _f32p, _i, _i]
+        L.oracle_nag.argtypes = [_f32p, _i, _f32p, _i, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        L.oracle_torch_randn.argtypes = [_f32p, ctypes.c_uint64, ctypes.c_size_t]
+        L.oracle_torch_randn.restype = _i
+        L.oracle_f32_to_f16.argtypes = [_u16p, _f32p, ctypes.c_size_t]
+        L.oracle_f16_to_f32.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+        L.oracle_num_threads.restype = _i
+        _LIB = L
+    return _LIB
+
+
+def _c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def num_threads():
+    return lib().oracle_num_threads()
+
+
+def ref_attn_f32(q, k, v, H, Dh=128, npad=0):
+    """Reference fp32 two-pass attention (bench/flash_test.cu:10-32). q [Tq, H*Dh], k/v [Tk, H*Dh]."""
+    q, k, v = _c32(q), _c32(k), _c32(v)
+    out = np.empty_like(q)
+    lib().oracle_ref_attn_f32(out, q.shape[1], q, q.shape[1], k, k.shape[1], v, v.shape[1], q.shape[0], k.shape[0],
+                              H, Dh, npad)
+    return out
+
+
+def attn_f64(q, k, v, H, Dh=128, npad=0, causal=False, scale=0.0):
+    """Double-accumulation golden attention (optionally causal)."""
+    q, k, v = _c32(q), _c32(k), _c32(v)
+    out = np.empty((q.shape[0], H * Dh), np.float32)
+    lib().oracle_attn_f64(out, out.shape[1], q, q.shape[1], k, k.shape[1], v, v.shape[1], q.shape[0], k.shape[0],
+                          H, Dh, int(causal), npad, scale)
+    return out
+
+
+def attn_f16sem(q, k, v, H, npad=0, out16=True):
+    """Emulation of the reference's fp16 tensor-core semantics (engine/src/tcflash.cuh)."""
+    q, k, v = _c32(q), _c32(k), _c32(v)
+    out = np.empty((q.shape[0], H * 128), np.float32)
+    lib().oracle_attn_f16sem(out, out.shape[1], q, q.shape[1], k, k.shape[1], v, v.shape[1], q.shape[0], k.shape[0],
+                             H, npad, int(out16))
+    return out
+
+
+def rmsnorm_rows(x, w_bf16=None, eps=1e-6, dim=128):
+    """Per-row RMSNorm over rows of `dim` (engine/src/kernels.cu:656-666); returns a new array."""
+    x = _c32(x)
+    y = np.empty_like(x)
+    rows = x.size // dim
+    wp = None
+    if w_bf16 is not None:
+        w_bf16 = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+        wp = w_bf16.ctypes.data
+    lib().oracle_rmsnorm_rows(y, x, wp, rows, dim, eps)
+    return y
+
+
+def rope_half(x, H, cos_t, sin_t, Dh=128):
+    """Rotate-half RoPE on x [T, ld] (engine/src/kernels.cu:759-772); returns a new array."""
+    y = _c32(x).copy()
+    T = y.shape[0]
+    lib().oracle_rope_half(y, y.shape[1], T, H, Dh, _c32(cos_t), _c32(sin_t))
+    return y
+
+
+def cosmos_rope(Hp, Wp):
+    """Cosmos 3D RoPE tables cos, sin [Hp*Wp, 64] (engine/src/dit.cu:196-215)."""
+    c = np.empty((Hp * Wp, 64), np.float32)
+    s = np.empty((Hp * Wp, 64), np.float32)
+    lib().oracle_cosmos_rope(c, s, Hp, Wp)
+    return c, s
+
+
+def nag(a, an, s=5.0, tau=2.5, alpha=0.25):
+    """NAG combine per row (engine/src/dit.cu:295-324); returns a new array."""
+    y = _c32(a).copy()
+    an = _c32(an)
+    lib().oracle_nag(y, y.shape[1], an, an.shape[1], y.shape[0], y.shape[1], s, tau, alpha)
+    return y
+
+
+def torch_randn(seed, n):
+    """Bit-exact torch.manual_seed(seed); torch.randn(n) (engine/src/pipeline.cu:17-64), n >= 16."""
+    out = np.empty(n, np.float32)
+    if lib().oracle_torch_randn(out, seed, n) != 0:
+        raise ValueError("torch_randn restatement needs n >= 16")
+    return out
+
+
+def to_f16_bits(x):
+    x = _c32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_f32_to_f16(out.reshape(-1), x.reshape(-1), x.size)
+    return out

@@ -1,0 +1,289 @@
+"""GPU parity of the HIP attention path against the CPU oracle (double-accumulation softmax attention).
+
+Tolerance: max-abs <= 2e-3 and mean-abs <= 2e-4 against the fp32 reference,
+on identical seeded inputs. Cases follow the reference harnesses (bench/tfa_test.cu:69-76 shapes,
+Q,K ~ N(0, 1.5), V ~ N(0, 1)) and the BASELINE configs 1-4.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kiln_amd
+import oracle
+from tests.helpers import assert_close, errors, f16_round, randn
+
+pytestmark = pytest.mark.gpu
+H, D = 16, 128
+DEV = "cuda:0"
+
+
+def emulator_bar(emu, ref):
+    """Bar for stress inputs outside the BASELINE configs (peaky softmax): the error that the reference's
+    fp16 semantics (oracle.attn_f16sem) itself has on the same inputs, plus one fp16 ulp of the largest
+    output for max-abs (the kernel and the emulator may round an output to neighbouring fp16 values),
+    1.25x for mean-abs; never below the BASELINE bar."""
+    emx, emn, _ = errors(emu, ref)
+    top = float(np.abs(ref).max())
+    ulp = 2.0 ** (np.floor(np.log2(max(top, 2.0 ** -14))) - 10)
+    return dict(max_abs=max(2e-3, emx + ulp), mean_abs=max(2e-4, 1.25 * emn))
+
+
+def _qkv(seed, Tq, Tk, scale_qk=1.5):
+    q = randn(seed, Tq, H * D, scale=scale_qk)
+    k = randn(seed + 1, Tk, H * D, scale=scale_qk)
+    v = randn(seed + 2, Tk, H * D)
+    return q, k, v
+
+
+# ---- config 1: plain self-attention, fp16 Q/K/V ~ N(0,1) from torch_randn(0, 3*1536*2048) ----
+def test_cfg1_plain_self_attention_f16(gpu):
+    S = 1536
+    x = randn(0, 3 * S * H * D)
+    q, k, v = (f16_round(t.reshape(S, H * D)) for t in x.split(S * H * D))
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), H)
+    for od in (torch.float16, torch.float32):
+        out = torch.empty(S, H * D, dtype=od, device=DEV)
+        kiln_amd.attn_f16in(out, q.half().to(DEV), k.half().to(DEV), v.half().to(DEV), 1, S, S, H)
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), ref, f"cfg1 S=1536 out={od}")
+
+
+# ---- drop-ins: the reference harness shapes (bench/tfa_test.cu:69-76) through attention16/attention ----
+TFA_SHAPES = [(1536, 1536, 0), (1536, 26, 486), (1000, 1000, 0), (1000, 77, 0), (3952, 3952, 0)]
+
+
+@pytest.mark.parametrize("Tq,Tk,npad", TFA_SHAPES)
+def test_dropin_attention16_tfa_shapes(gpu, Tq, Tk, npad):
+    """The reference harness draws Q,K ~ N(0, 1.5) (bench/tfa_test.cu:39-42): scores have std 2.25, so
+    the fp16 rounding of Q and K alone (the CUDA path's semantics) moves outputs by ~2e-3. These shapes
+    are not BASELINE configs; the bar here is the reference's own: the error of the fp16-semantics
+    emulator on the same inputs (x1.25), and rel_l2 at the published 6.9e-4 (README.md:570)."""
+    q, k, v = _qkv(3, Tq, Tk)
+    rows = np.random.default_rng(Tq).choice(Tq, size=min(Tq, 512), replace=False)
+    qn, kn, vn = q.numpy()[rows], k.numpy(), v.numpy()
+    ref = oracle.attn_f64(qn, kn, vn, H, npad=npad)
+    emu32 = oracle.attn_f16sem(qn, kn, vn, H, npad=npad, out16=False)
+    emu16 = oracle.attn_f16sem(qn, kn, vn, H, npad=npad, out16=True)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out16 = torch.empty(Tq, H * D, dtype=torch.float16, device=DEV)
+    kiln_amd.attention16(out16, qd, kd, vd, Tq, Tk, H, D, npad=npad)
+    out32 = torch.empty(Tq, H * D, dtype=torch.float32, device=DEV)
+    kiln_amd.attention(out32, qd, kd, vd, Tq, Tk, H, D, causal=False, npad=npad)
+    torch.cuda.synchronize()
+    for name, got, emu in (("attention16", out16.float().cpu().numpy()[rows], emu16),
+                           ("attention", out32.cpu().numpy()[rows], emu32)):
+        emx, emn, erl = errors(emu, ref)
+        assert_close(got, ref, f"{name} {Tq}x{Tk}+{npad} (emulator max {emx:.2e} mean {emn:.2e} rel {erl:.2e})",
+                     max_abs=max(2e-3, 1.25 * emx), mean_abs=max(2e-4, 1.25 * emn))
+        assert errors(got, ref)[2] <= max(6.9e-4, 1.25 * erl)
+
+
+def test_dropin_matches_fp16_semantics_emulator(gpu):
+    """Per element, the kernel must sit at the fp16-semantics emulator, far inside the fp32 bar."""
+    Tq, Tk = 256, 333
+    q, k, v = _qkv(11, Tq, Tk)
+    emu = oracle.attn_f16sem(q.numpy(), k.numpy(), v.numpy(), H, out16=False)
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), H)
+    out = torch.empty(Tq, H * D, dtype=torch.float32, device=DEV)
+    kiln_amd.attention(out, q.to(DEV), k.to(DEV), v.to(DEV), Tq, Tk, H, D)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    mx_e, mn_e, _ = errors(got, emu)
+    mx_r, mn_r, _ = errors(emu, ref)
+    print(f"[parity] kernel vs emulator max {mx_e:.2e} mean {mn_e:.2e}; emulator vs f64 max {mx_r:.2e} mean {mn_r:.2e}")
+    assert mn_e <= mn_r, "kernel deviates from the fp16 semantics more than fp16 itself deviates from fp32"
+    assert mx_e <= 1e-3
+
+
+# ---- configs 2 and 4: fused DiT self-attention (QK-RMSNorm + 3D RoPE), CFG batch 2 ----
+def _dit_inputs(seed, T, B, wlow=None, dtype=torch.float16):
+    """Q/K/V = X W^T with X ~ N(0,1) [B*T, 2048], W ~ U(+-1/sqrt(2048)) (torch Linear init)."""
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(B * T, H * D, generator=g)
+    outs = []
+    for i in range(3):
+        W = (torch.rand(H * D, H * D, generator=g) * 2 - 1) / np.sqrt(H * D)
+        outs.append((X @ W.T).to(dtype))
+    if wlow is None:
+        qw = torch.ones(D, dtype=torch.bfloat16)
+        kw = torch.ones(D, dtype=torch.bfloat16)
+    else:
+        qw = (torch.rand(D, generator=g) * 2 + 1).to(torch.bfloat16)
+        kw = (torch.rand(D, generator=g) * 2 + 1).to(torch.bfloat16)
+    return outs, qw, kw
+
+
+def _dit_reference(q, k, v, qw, kw, cos, sin, B, T, rows):
+    """oracle: rmsnorm(Q), rmsnorm(K) per head, rope both, attention (engine/src/dit.cu:464-470)."""
+    outs = []
+    qwb = qw.view(torch.int16).numpy().view(np.uint16)
+    kwb = kw.view(torch.int16).numpy().view(np.uint16)
+    for b in range(B):
+        qb = q[b * T:(b + 1) * T].float().numpy()
+        kb = k[b * T:(b + 1) * T].float().numpy()
+        vb = v[b * T:(b + 1) * T].float().numpy()
+        qn = oracle.rope_half(oracle.rmsnorm_rows(qb, qwb).reshape(T, H * D), H, cos, sin)
+        kn = oracle.rope_half(oracle.rmsnorm_rows(kb, kwb).reshape(T, H * D), H, cos, sin)
+        outs.append((oracle.attn_f64(qn[rows], kn, vb, H), (qn[rows], kn, vb)))
+    return outs
+
+
+@pytest.mark.parametrize("Hp,Wp,wvar", [(32, 48, None), (32, 48, "u13"), (64, 64, None)])
+def test_dit_self_attention_fused(gpu, Hp, Wp, wvar):
+    T, B = Hp * Wp, 2
+    (q, k, v), qw, kw = _dit_inputs(5, T, B, wvar)
+    cos, sin = oracle.cosmos_rope(Hp, Wp)
+    rows = np.sort(np.random.default_rng(T).choice(T, size=min(T, 384), replace=False))
+    refs = _dit_reference(q, k, v, qw, kw, cos, sin, B, T, rows)
+    out = torch.empty(B * T, H * D, dtype=torch.float16, device=DEV)
+    rope = (torch.from_numpy(cos).to(DEV), torch.from_numpy(sin).to(DEV))
+    kiln_amd.dit_self_attn(out, q.to(DEV), k.to(DEV), v.to(DEV), B, T, H, qw.to(DEV), kw.to(DEV), rope)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    for b in range(B):
+        ref, normed = refs[b]
+        # norm weights 1 (torch RMSNorm init) = the BASELINE configs 2/4: strict bar; U(1,3): stress
+        bar = {} if wvar is None else emulator_bar(oracle.attn_f16sem(*normed, H), ref)
+        assert_close(o[b * T:(b + 1) * T][rows], ref, f"DiT self T={T} b={b} w={wvar}", **bar)
+
+
+def test_dit_self_attention_fp32_inputs(gpu):
+    """The reference's own DiT path hands fp32 Q/K/V to attention (engine/src/dit.cu:501-506)."""
+    Hp, Wp, B = 16, 24, 2
+    T = Hp * Wp
+    (q, k, v), qw, kw = _dit_inputs(9, T, B, None, dtype=torch.float32)
+    cos, sin = oracle.cosmos_rope(Hp, Wp)
+    rows = np.arange(T)
+    refs = _dit_reference(q, k, v, qw, kw, cos, sin, B, T, rows)
+    out = torch.empty(B * T, H * D, dtype=torch.float32, device=DEV)
+    rope = (torch.from_numpy(cos).to(DEV), torch.from_numpy(sin).to(DEV))
+    kiln_amd.dit_self_attn(out, q.to(DEV), k.to(DEV), v.to(DEV), B, T, H, qw.to(DEV), kw.to(DEV), rope)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    for b in range(B):
+        assert_close(o[b * T:(b + 1) * T], refs[b][0], f"DiT self fp32-in T={T} b={b}")
+
+
+# ---- config 3: cross-attention over 512 context tokens, positive + negative, NAG ----
+@pytest.mark.parametrize("L,npad,wvar", [(512, 0, None), (26, 486, None), (512, 0, "u13")])
+def test_cross_attention_nag(gpu, L, npad, wvar):
+    T, B = 1536, 2
+    g = torch.Generator().manual_seed(21)
+    qraw = (torch.randn(B * T, H * D, generator=g)).half()
+    qw = torch.ones(D, dtype=torch.bfloat16) if wvar is None else (torch.rand(D, generator=g) * 2 + 1).to(torch.bfloat16)
+    ctx = []
+    for c in range(3):  # b=0 positive, b=1 uncond/negative, NAG negative
+        kk = torch.randn(L, H * D, generator=g)
+        vv = torch.randn(L, H * D, generator=g)
+        kk = torch.from_numpy(oracle.rmsnorm_rows(kk.numpy()).reshape(L, H * D))  # cache_context's K norm
+        ctx.append((kk.half(), vv.half()))
+    qwb = qw.view(torch.int16).numpy().view(np.uint16)
+    qn = [oracle.rmsnorm_rows(qraw[b * T:(b + 1) * T].float().numpy(), qwb).reshape(T, H * D) for b in range(B)]
+    refs = [oracle.attn_f64(qn[b], ctx[b][0].float().numpy(), ctx[b][1].float().numpy(), H, npad=npad)
+            for b in range(B)]
+    ref_neg = oracle.attn_f64(qn[0], ctx[2][0].float().numpy(), ctx[2][1].float().numpy(), H, npad=npad)
+    ref0 = oracle.nag(refs[0], ref_neg, 5.0, 2.5, 0.25)
+    # fp16 semantics on the same inputs: per-attention bars, and the NAG output of emulated attentions
+    emus = [oracle.attn_f16sem(qn[b], ctx[b][0].float().numpy(), ctx[b][1].float().numpy(), H, npad=npad)
+            for b in range(B)]
+    emu_neg = oracle.attn_f16sem(qn[0], ctx[2][0].float().numpy(), ctx[2][1].float().numpy(), H, npad=npad)
+    emu0 = oracle.nag(emus[0], emu_neg, 5.0, 2.5, 0.25)
+    strict = wvar is None
+
+    kvps = [kiln_amd.kv_prepare(kk.to(DEV), vv.to(DEV), H) for kk, vv in ctx]
+    out = torch.empty(B * T, H * D, dtype=torch.float16, device=DEV)
+    out_neg = torch.empty(T, H * D, dtype=torch.float16, device=DEV)
+    kiln_amd.cross_attn_nag(out, qraw.to(DEV), B, T, H, kvps[:2], [L, L], [npad, npad], q_norm_w=qw.to(DEV),
+                            kvp_neg=kvps[2], Lk_neg=L, npad_neg=npad, out_neg=out_neg)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    assert_close(out_neg.float().cpu().numpy(), ref_neg, f"cross NAG-neg L={L}+{npad}",
+                 **({} if strict else emulator_bar(emu_neg, ref_neg)))
+    assert_close(o[T:], refs[1], f"cross b=1 L={L}+{npad}", **({} if strict else emulator_bar(emus[1], refs[1])))
+    # the NAG blend amplifies attention error (by up to (2s-1)*alpha + 1-alpha = 3): bar from the same blend of
+    # fp16-semantics attentions, never below the BASELINE bar
+    assert_close(o[:T], ref0, f"cross+NAG b=0 L={L}+{npad}", **emulator_bar(emu0, ref0))
+
+
+# ---- edge cases ----
+@pytest.mark.parametrize("Tq,Tk,npad", [(1, 1, 0), (1, 64, 0), (65, 63, 0), (129, 65, 3), (7, 1, 100), (300, 0, 5)])
+def test_edge_shapes(gpu, Tq, Tk, npad):
+    q, k, v = _qkv(31, Tq, max(Tk, 1), scale_qk=1.0)
+    k, v = k[:Tk], v[:Tk]
+    if Tk == 0:
+        ref = np.zeros((Tq, H * D), np.float32)
+    else:
+        ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), H, npad=npad)
+    out = torch.full((Tq, H * D), float("nan"), dtype=torch.float32, device=DEV)
+    kd = k.to(DEV) if Tk else torch.empty(1, H * D, device=DEV)
+    vd = v.to(DEV) if Tk else torch.empty(1, H * D, device=DEV)
+    kiln_amd.attention(out, q.to(DEV), kd, vd, Tq, Tk, H, D, npad=npad)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, f"edge Tq={Tq} Tk={Tk} npad={npad}")
+
+
+def test_explicit_zero_keys_equal_npad(gpu):
+    """npad analytic zero keys == the same zero rows present explicitly (tcflash.cuh:136-147)."""
+    Tq, L, npad = 200, 40, 88
+    q, k, v = _qkv(41, Tq, L, scale_qk=1.0)
+    kz = torch.cat([k, torch.zeros(npad, H * D)])
+    vz = torch.cat([v, torch.zeros(npad, H * D)])
+    a = torch.empty(Tq, H * D, device=DEV)
+    b = torch.empty(Tq, H * D, device=DEV)
+    kiln_amd.attention(a, q.to(DEV), k.to(DEV), v.to(DEV), Tq, L, H, D, npad=npad)
+    kiln_amd.attention(b, q.to(DEV), kz.to(DEV), vz.to(DEV), Tq, L + npad, H, D)
+    torch.cuda.synchronize()
+    assert_close(a.cpu().numpy(), b.cpu().numpy(), "npad vs explicit zeros", max_abs=1e-3, mean_abs=1e-4)
+
+
+def test_unsupported_and_invalid(gpu):
+    q = torch.zeros(8, H * 64, device=DEV)
+    out = torch.zeros(8, H * 64, dtype=torch.float16, device=DEV)
+    with pytest.raises(kiln_amd.KilnError) as e:
+        kiln_amd.attention16(out, q, q, q, 8, 8, H, 64)
+    assert e.value.status == kiln_amd.KILN_EUNSUPPORTED
+    with pytest.raises(kiln_amd.KilnError) as e:
+        kiln_amd.attention(torch.zeros(8, H * D, device=DEV), torch.zeros(8, H * D, device=DEV),
+                           torch.zeros(8, H * D, device=DEV), torch.zeros(8, H * D, device=DEV), 8, 0, H, D)
+    assert e.value.status == kiln_amd.KILN_EINVAL
+
+
+# ---- exact fp32 path (causal / Dh != 128 / fp32 mode) ----
+@pytest.mark.parametrize("Dh,causal,npad", [(64, False, 0), (128, True, 0), (64, True, 0), (80, False, 7)])
+def test_exact_attention(gpu, Dh, causal, npad):
+    Tq, Tk, Hh = 150, 150, 4
+    q = randn(51, Tq, Hh * Dh)
+    k = randn(52, Tk, Hh * Dh)
+    v = randn(53, Tk, Hh * Dh)
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), Hh, Dh=Dh, npad=npad, causal=causal)
+    out = torch.empty(Tq, Hh * Dh, device=DEV)
+    kiln_amd.attention(out, q.to(DEV), k.to(DEV), v.to(DEV), Tq, Tk, Hh, Dh, causal=causal, npad=npad)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, f"exact Dh={Dh} causal={causal}", max_abs=1e-5, mean_abs=1e-6)
+
+
+# ---- the bandwidth-bound ops around attention ----
+def test_rmsnorm_rope_nag_kernels(gpu):
+    T = 96
+    x = randn(61, T, H * D)
+    w = (torch.rand(D, generator=torch.Generator().manual_seed(62)) * 2 + 1).to(torch.bfloat16)
+    wb = w.view(torch.int16).numpy().view(np.uint16)
+    cos, sin = oracle.cosmos_rope(8, 12)
+    ref = oracle.rope_half(oracle.rmsnorm_rows(x.numpy(), wb).reshape(T, H * D), H, cos, sin)
+    xd = x.to(DEV)
+    kiln_amd.rmsnorm(xd, xd, w.to(DEV), rows=T * H, dim=D)
+    kiln_amd.rope_half(xd, T, H, D, torch.from_numpy(cos).to(DEV), torch.from_numpy(sin).to(DEV))
+    torch.cuda.synchronize()
+    assert_close(xd.cpu().numpy(), ref, "rmsnorm+rope", max_abs=1e-5, mean_abs=1e-6)
+    c2, s2 = kiln_amd.cosmos_rope_tables(8, 12)
+    assert np.array_equal(c2.numpy(), cos) and np.array_equal(s2.numpy(), sin)
+
+    a = randn(63, T, H * D) * 0.1
+    an = randn(64, T, H * D) * 0.1
+    ref = oracle.nag(a.numpy(), an.numpy())
+    for dt, tol in ((torch.float32, 1e-5), (torch.float16, 2e-3)):
+        ad = a.to(dt).to(DEV)
+        kiln_amd.nag_combine(ad, an.to(dt).to(DEV))
+        torch.cuda.synchronize()
+        r = oracle.nag(a.to(dt).float().numpy(), an.to(dt).float().numpy())
+        assert_close(ad.float().cpu().numpy(), r, f"nag {dt}", max_abs=tol, mean_abs=tol / 10)

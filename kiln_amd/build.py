@@ -21,7 +21,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
+    "-fno-honor-nans", "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
 ]
 
 

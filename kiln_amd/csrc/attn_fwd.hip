@@ -20,14 +20,17 @@
 //    tile's max exceeds it by more than 8 (log2 units), so P <= 2^8 stays far inside fp16 range.
 //  * 1-D grid with an XCD-aware block -> work mapping: consecutive work items (the query tiles of one
 //    head) land on the same XCD and share its L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "internal.hpp"
 
 namespace kiln {
 
-constexpr int BM = 128;
-constexpr int NTHR = 256;
 constexpr float RESCALE_TH = 8.0f;
+#ifndef KILN_SCHED
+#define KILN_SCHED 0
+#endif
 
 struct AttnParams {
     AttnJob job[MAX_JOBS];
@@ -65,169 +68,107 @@ __device__ __forceinline__ void store4<float>(float* dst, float a, float b, floa
     }
 }
 
-template <typename InT, typename OutT, bool QNORM, bool ROPE>
-__global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * KV_TILE_H];  // 2 stages x (K 16 KB + V 16 KB)
+__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int l32 = lane & 31, hh = lane >> 5;
+// ---- shared pieces of the two kernels ----
 
-    // blocks are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8): give each XCD a
-    // contiguous range of work items so the query tiles of one head share that XCD's L2.
-    const int w = (int)(blockIdx.x & 7) * p.per + (int)(blockIdx.x >> 3);
-    if (w >= p.total) return;
-    const int qt = w % p.qtiles;
-    const int rest = w / p.qtiles;
-    const int h = rest % p.H;
-    const int jb = rest / p.H;
-    const AttnJob J = p.job[jb];
+// Work item of block b. Blocks are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8):
+// each XCD gets a contiguous range of work items, so the query tiles of one head share its L2.
+struct Work {
+    int qt, h, jb;
+};
+__device__ __forceinline__ bool decode_work(const AttnParams& p, Work& w) {
+    const int i = (int)(blockIdx.x & 7) * p.per + (int)(blockIdx.x >> 3);
+    if (i >= p.total) return false;
+    w.qt = i % p.qtiles;
+    const int rest = i / p.qtiles;
+    w.h = rest % p.H;
+    w.jb = rest / p.H;
+    return true;
+}
 
-    // ---- Q tile: this lane's query row, d chunks {16s + 8hh .. +8}, s = 0..7 -> B operands ----
-    const int row = qt * BM + wv * 32 + l32;
-    const bool qin = row < p.Tq;
-    half8 qreg[8];
-    {
-        float x[8][8];
-        const InT* qr = reinterpret_cast<const InT*>(J.q) + (size_t)(qin ? row : 0) * p.ldq + h * HD + 8 * hh;
+// Q tile of one lane: query `row`, d chunks {16s + 8hh .. +8} for s = 0..7 (the B operands of S^T = K Q^T),
+// RMSNorm and RoPE applied in fp32, pre-scaled by log2(e)/sqrt(128), rounded once to fp16.
+template <typename InT, bool QNORM, bool ROPE>
+__device__ __forceinline__ void load_q(const AttnParams& p, const void* q, int row, bool qin, int h, int hh,
+                                       half8 (&qreg)[8]) {
+    float x[8][8];
+    const InT* qr = reinterpret_cast<const InT*>(q) + (size_t)(qin ? row : 0) * p.ldq + h * HD + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        if (qin) load8(qr + 16 * s, x[s]);
+        else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[s][e] = 0.f;
+        }
+    }
+    if constexpr (QNORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss += x[s][e] * x[s][e];
+        ss = pair_sum(ss);
+        const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            if (qin) load8(qr + 16 * s, x[s]);
-            else {
+            const uint16_t* wp = p.qw + 16 * s + 8 * hh;
 #pragma unroll
-                for (int e = 0; e < 8; e++) x[s][e] = 0.f;
-            }
+            for (int e = 0; e < 8; e++) x[s][e] = x[s][e] * r * bf16_to_f32(wp[e]);
         }
-        if constexpr (QNORM) {
-            float ss = 0.f;
+    }
+    if constexpr (ROPE) {
+        if (qin) {
 #pragma unroll
-            for (int s = 0; s < 8; s++)
+            for (int s = 0; s < 4; s++) {
+                float c[8], sn[8];
+                load8(p.rcos + (size_t)row * 64 + 16 * s + 8 * hh, c);
+                load8(p.rsin + (size_t)row * 64 + 16 * s + 8 * hh, sn);
 #pragma unroll
-                for (int e = 0; e < 8; e++) ss += x[s][e] * x[s][e];
-            ss = pair_sum(ss);
-            const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const uint16_t* wp = p.qw + 16 * s + 8 * hh;
-#pragma unroll
-                for (int e = 0; e < 8; e++) x[s][e] = x[s][e] * r * bf16_to_f32(wp[e]);
-            }
-        }
-        if constexpr (ROPE) {
-            if (qin) {
-#pragma unroll
-                for (int s = 0; s < 4; s++) {
-                    float c[8], sn[8];
-                    load8(p.rcos + (size_t)row * 64 + 16 * s + 8 * hh, c);
-                    load8(p.rsin + (size_t)row * 64 + 16 * s + 8 * hh, sn);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        const float a = x[s][e], b = x[s + 4][e];
-                        x[s][e] = a * c[e] - b * sn[e];
-                        x[s + 4][e] = b * c[e] + a * sn[e];
-                    }
+                for (int e = 0; e < 8; e++) {
+                    const float a = x[s][e], b = x[s + 4][e];
+                    x[s][e] = a * c[e] - b * sn[e];
+                    x[s + 4][e] = b * c[e] + a * sn[e];
                 }
             }
         }
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[s][e] *= p.qscale;
-            qreg[s] = to_half8(x[s]);
-        }
     }
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[s][e] *= p.qscale;
+        qreg[s] = to_half8(x[s]);
+    }
+}
 
-    const int Tk = J.Tk;
-    const int nt = kv_tiles(Tk);
-    const uint16_t* kvh = J.kv + (size_t)h * kv_head_stride(Tk);
+// accumulator item i of a 32-key half tile holds key 32*jh + 8*(i/4) + 4*hh + i%4
+__device__ __forceinline__ void mask_half(int jh, int Tk, int hh, floatx16& a) {
+    const int kbase = jh * 32 + 4 * hh;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        if (kbase + 8 * (i / 4) + (i % 4) >= Tk) a[i] = -INFINITY;
+}
 
-    u32x4 pre[8];
-    auto gload = [&](int j) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(kvh + (size_t)j * KV_TILE_H);
-#pragma unroll
-        for (int i = 0; i < 8; i++) pre[i] = src[tid + NTHR * i];
-    };
-    auto lstore = [&](int stage) {
-        u32x4* dst = reinterpret_cast<u32x4*>(lds + stage * KV_TILE_H);
-#pragma unroll
-        for (int i = 0; i < 8; i++) dst[tid + NTHR * i] = pre[i];
-    };
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
-    floatx16 o[4];
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) o[db][i] = 0.f;
-    float m = -INFINITY, l = 0.f;
-
-    for (int j = 0; j < nt; j++) {
-        if (j + 1 < nt) gload(j + 1);
-        const _Float16* ks = lds + (j & 1) * KV_TILE_H;
-        const _Float16* vs = ks + TILE_H;
-
-        // S^T[key][query] for the tile's two 32-key blocks
-        floatx16 s0, s1;
-#pragma unroll
-        for (int i = 0; i < 16; i++) { s0[i] = 0.f; s1[i] = 0.f; }
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const half8 a0 = *reinterpret_cast<const half8*>(ks + ((0 * 8 + s) * 64 + lane) * 8);
-            const half8 a1 = *reinterpret_cast<const half8*>(ks + ((1 * 8 + s) * 64 + lane) * 8);
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[s], s1, 0, 0, 0);
-        }
-        // accumulator item i of key block kb holds key j*64 + kb*32 + 8*(i/4) + 4*hh + i%4
-        if ((j + 1) * KT > Tk) {
-            const int kbase = j * KT + 4 * hh;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int key = kbase + 8 * (i / 4) + (i % 4);
-                if (key >= Tk) s0[i] = -INFINITY;
-                if (key + 32 >= Tk) s1[i] = -INFINITY;
-            }
-        }
-
-        float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-        for (int i = 1; i < 16; i++) mx = fmaxf(mx, fmaxf(s0[i], s1[i]));
-        mx = pair_max(mx);
-        const float mnew = fmaxf(m, mx);
-        if (__builtin_amdgcn_ballot_w64(mnew > m + RESCALE_TH)) {
-            const float corr = __builtin_amdgcn_exp2f(m - mnew);
-#pragma unroll
-            for (int db = 0; db < 4; db++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) o[db][i] *= corr;
-            l *= corr;
-            m = mnew;
-        }
-
-        half8 pb[4];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float e0 = __builtin_amdgcn_exp2f(s0[i] - m);
-            const float e1 = __builtin_amdgcn_exp2f(s1[i] - m);
-            l += e0 + e1;
-            pb[i / 8][i % 8] = (_Float16)e0;
-            pb[2 + i / 8][i % 8] = (_Float16)e1;
-        }
-
+// lazy rescale: only when the running max grows by more than RESCALE_TH (wave-uniform branch)
+__device__ __forceinline__ void maybe_rescale(float mx, float& m, float& l, floatx16 (&o)[4]) {
+    const float mnew = fmaxf(m, mx);
+    if (__builtin_amdgcn_ballot_w64(mnew > m + RESCALE_TH)) {
+        const float corr = __builtin_amdgcn_exp2f(m - mnew);
 #pragma unroll
         for (int db = 0; db < 4; db++)
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const half8 a = *reinterpret_cast<const half8*>(vs + ((db * 4 + t) * 64 + lane) * 8);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[t], o[db], 0, 0, 0);
-            }
-
-        if (j + 1 < nt) lstore((j + 1) & 1);
-        __syncthreads();
+            for (int i = 0; i < 16; i++) o[db][i] *= corr;
+        l *= corr;
+        m = mnew;
     }
+}
 
-    // epilogue: full row sum (lane pair), npad zero keys, normalize, store
+// full row sum (lane pair), npad zero keys (tcflash.cuh:136-147), normalize, store this lane's row
+template <typename OutT>
+__device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, int row, bool qin, int h, int hh,
+                                         float m, float l, const floatx16 (&o)[4]) {
     float lt = pair_sum(l);
     float sc = 1.f;
     if (J.npad) {
@@ -247,6 +188,300 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
                          o[db][4 * g + 3] * inv, pairs);
 }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
+#define KILN_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (0xF << 8) | (((N) >> 4) << 14))
+
+// ------------------------------------------------------------------------------------------------
+// The kernel: 4 waves x 32 query rows (BM = 128) per workgroup, two workgroups per CU (2 waves per
+// SIMD, from independent workgroups). Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB)
+// through an NS-stage LDS ring filled by direct global->LDS DMA (global_load_lds_dwordx4: no staging
+// registers, no ds_write), NS-1 half tiles ahead of use.
+//
+// Scores are kept relative to the running max m: each QK^T MFMA chain starts from C = -m, so S - m
+// comes out of the matrix core and p = 2^(S - m) needs one v_exp per score.
+//
+// Software pipeline, per half tile j (S_j - m and max(S_j) in registers, K_{j+1} operands in
+// registers, half tiles j .. j+NS-2 resident or in flight):
+//   [rare: rescale O, l, m]                                         (the only branch)
+//   V_j reads | DMA tile j+NS-1 | QK_{j+1} MFMAs interleaved with exp/cvt/row-sum of S_j |
+//   wait tile j+2, barrier | K_{j+2} reads | PV_j MFMAs interleaved with max(S_{j+1})
+// so each wave always has an independent MFMA chain in flight under its VALU work, and every LDS
+// read is issued one phase before its use.
+// ------------------------------------------------------------------------------------------------
+#ifndef KILN_NS
+#define KILN_NS 5
+#endif
+#ifndef KILN_PIN
+#define KILN_PIN 1
+#endif
+#if KILN_PIN
+#define KILN_FENCE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define KILN_FENCE() ((void)0)
+#endif
+#ifndef KILN_NEGM
+#define KILN_NEGM 0
+#endif
+typedef __attribute__((address_space(3))) half8 lds_half8;
+constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = KILN_NS;
+constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile (4)
+static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
+
+#if KILN_CLOCK
+__device__ long long g_clk[16384][2];  // per workgroup: shader cycles, 100 MHz ticks (debug builds only)
+#endif
+
+template <typename InT, typename OutT, bool QNORM, bool ROPE>
+__global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
+#if KILN_CLOCK
+    const long long clk0 = __builtin_amdgcn_s_memtime(), rt0 = __builtin_amdgcn_s_memrealtime();
+#endif
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];  // NS x 16 KB
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hh = lane >> 5;
+    Work W;
+    if (!decode_work(p, W)) return;
+    const AttnJob J = p.job[W.jb];
+
+    const int row = W.qt * BM + wv * 32 + (lane & 31);
+    const bool qin = row < p.Tq;
+    half8 qreg[8];
+    load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, hh, qreg);
+
+    const int Tk = J.Tk;
+    const int nh = (Tk + 31) / 32;  // half tiles holding real keys
+    const _Float16* kvh = reinterpret_cast<const _Float16*>(J.kv) + (size_t)W.h * kv_head_stride(Tk);
+    const uint32_t lds_base = (uint32_t)(size_t)(__attribute__((address_space(3))) _Float16*)lds;
+
+    // half tile jh -> stage: this thread's 16-byte pieces tid + NTHR*i; the wave's 64 lanes write 1 KB
+    // of contiguous LDS at the wave-uniform base the DMA takes from M0
+    auto dma = [&](int jh, int stage) {
+        const _Float16* src = kvh + (size_t)jh * HT_H + tid * 8;
+        _Float16* dst = lds + stage * HT_H + wv * 512;
+#pragma unroll
+        for (int i = 0; i < DMA_PER_HT; i++)
+            __builtin_amdgcn_global_load_lds((const void*)(src + i * NTHR * 8),
+                                             (__attribute__((address_space(3))) void*)(dst + i * NTHR * 8), 16, 0, 0);
+    };
+    // operand reads through 32-bit LDS byte addresses: base + immediate offsets fold into ds_read_b128
+    auto kptr = [&](int stage) {
+        return reinterpret_cast<const lds_half8*>((size_t)(lds_base + stage * HT_H * 2 + lane * 16));
+    };
+    auto read_k = [&](int stage, half8 (&ka)[8]) {
+        const lds_half8* kp = kptr(stage);
+#pragma unroll
+        for (int s = 0; s < 8; s++) ka[s] = kp[s * 64];
+    };
+    auto read_v = [&](int stage, half8 (&va)[8]) {
+        const lds_half8* vp = kptr(stage) + 32 * HD / 8;
+#pragma unroll
+        for (int g = 0; g < 8; g++) va[g] = vp[g * 64];
+    };
+    auto max16 = [](const floatx16& a) {
+        const float x0 = fmaxf(fmaxf(a[0], a[1]), a[2]), x1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
+        const float x2 = fmaxf(fmaxf(a[6], a[7]), a[8]), x3 = fmaxf(fmaxf(a[9], a[10]), a[11]);
+        const float x4 = fmaxf(fmaxf(a[12], a[13]), a[14]);
+        return pair_max(fmaxf(fmaxf(fmaxf(x0, x1), x2), fmaxf(fmaxf(x3, x4), a[15])));
+    };
+
+    // prologue: half tiles 0 .. NS-2 in flight; wait for tiles 0 and 1
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++) dma(min(i, nh - 1), i);
+    KILN_WAIT_VMCNT((NS - 3) * DMA_PER_HT);
+    __builtin_amdgcn_s_barrier();
+
+    floatx16 o[4];
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[db][i] = 0.f;
+    float l = 0.f;
+    const half2v ones = {(_Float16)1.f, (_Float16)1.f};
+
+    half8 ka[8];  // K operands: [0,4) of the next QK chain are read a phase ahead of [4,8)
+#pragma unroll
+    for (int s = 0; s < 8; s++) ka[s] = kptr(0)[s * 64];
+    floatx16 sc;  // S_j (relative to m when KILN_NEGM)
+#pragma unroll
+    for (int i = 0; i < 16; i++) sc[i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; s++) sc = mfma32(ka[s], qreg[s], sc);
+    if (Tk < 32) mask_half(0, Tk, hh, sc);
+    float m = max16(sc);  // the first half tile sets the running max
+#if KILN_NEGM
+    floatx16 negm;  // -m in every accumulator slot: the C operand that starts each QK^T chain
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        sc[i] -= m;
+        negm[i] = -m;
+    }
+#endif
+    float mx = 0.f;  // max(S_j) - m
+#pragma unroll
+    for (int s = 0; s < 4; s++) ka[s] = kptr(1 % NS)[s * 64];
+
+    int st = 0;            // stage of half tile j
+    int st2 = NS - 1;      // stage that receives half tile j+NS-1
+    // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
+    //   rescale (rare) | K_{j+1}[4,8), V_j[t=0] reads | QK_{j+1} || exp S_j | wait tile j+2, barrier |
+    //   DMA tile j+NS-1 into the stage of tile j-1 | K_{j+2}[0,4), V_j[t=1] reads | PV_j || max S_{j+1}
+    // Every read of a stage completes before the barrier that precedes its refill: V_j[t=1] and the
+    // K_{j+1}[4,8) reads are consumed (waited on) before the next iteration's barrier.
+    auto step = [&](auto maskn_tag, int j) {
+        constexpr bool MASKN = decltype(maskn_tag)::value;
+        if (__builtin_amdgcn_ballot_w64(mx > RESCALE_TH)) {  // lazy rescale (rare)
+            const float d = fmaxf(mx, 0.f);
+            const float corr = __builtin_amdgcn_exp2f(-d);
+#pragma unroll
+            for (int db = 0; db < 4; db++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) o[db][i] *= corr;
+            l *= corr;
+            m += d;
+#if KILN_NEGM
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                sc[i] -= d;
+                negm[i] = -m;
+            }
+#endif
+        }
+#if KILN_NEGM
+        const float mofs = 0.f;  // sc already holds S - m
+#else
+        const float mofs = m;
+#endif
+        const int st1 = st == NS - 1 ? 0 : st + 1;
+        half8 va[4];
+        {
+            const lds_half8* kp = kptr(st1);
+#pragma unroll
+            for (int s = 4; s < 8; s++) ka[s] = kp[s * 64];
+            const lds_half8* vp = kptr(st) + 32 * HD / 8;
+#pragma unroll
+            for (int g = 0; g < 4; g++) va[g] = vp[g * 64];
+        }
+        KILN_FENCE();
+
+        // S_{j+1} on the matrix core while the VALU turns S_j into P_j
+#if KILN_NEGM
+        floatx16 sn = mfma32(ka[0], qreg[0], negm);
+#else
+        floatx16 sn = mfma32(ka[0], qreg[0], floatx16{});
+#endif
+        half8 pb[2];
+        float la = 0.f, lb = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            if (s > 0) sn = mfma32(ka[s], qreg[s], sn);
+            const float e0 = __builtin_amdgcn_exp2f(sc[2 * s] - mofs);
+            const float e1 = __builtin_amdgcn_exp2f(sc[2 * s + 1] - mofs);
+            pb[s / 4][(2 * s) % 8] = (_Float16)e0;
+            pb[s / 4][(2 * s + 1) % 8] = (_Float16)e1;
+            if (s & 1) {  // row sum of the fp16-rounded P values the PV MFMA consumes
+                const half2v p0 = {pb[s / 4][(2 * s - 2) % 8], pb[s / 4][(2 * s - 1) % 8]};
+                const half2v p1 = {pb[s / 4][(2 * s) % 8], pb[s / 4][(2 * s + 1) % 8]};
+                la = __builtin_amdgcn_fdot2(p0, ones, la, false);
+                lb = __builtin_amdgcn_fdot2(p1, ones, lb, false);
+            }
+        }
+        KILN_FENCE();
+
+        // tile j+2 landed in every wave; every wave is done with tile j-1
+        // only tiles j+3 .. j+NS-2 may be in flight; the peeled masking step (whose register spills are
+        // vector memory operations too) waits for everything
+        if constexpr (MASKN) KILN_WAIT_VMCNT(0);
+        else KILN_WAIT_VMCNT((NS - 4) * DMA_PER_HT);
+        __builtin_amdgcn_s_barrier();
+        dma(min(j + NS - 1, nh - 1), st2);  // into the stage of tile j-1
+        st2 = st2 == NS - 1 ? 0 : st2 + 1;
+        half8 vb[4];
+        {
+            const lds_half8* kp = kptr(st1 == NS - 1 ? 0 : st1 + 1);  // K_{j+2}; past the end: stale, unused
+#pragma unroll
+            for (int s = 0; s < 4; s++) ka[s] = kp[s * 64];
+            const lds_half8* vp = kptr(st) + 32 * HD / 8 + 4 * 64;
+#pragma unroll
+            for (int g = 0; g < 4; g++) vb[g] = vp[g * 64];
+        }
+        KILN_FENCE();
+
+        if constexpr (MASKN) mask_half(j + 1, Tk, hh, sn);
+#pragma unroll
+        for (int db = 0; db < 4; db++) o[db] = mfma32(va[db], pb[0], o[db]);
+#pragma unroll
+        for (int db = 0; db < 4; db++) o[db] = mfma32(vb[db], pb[1], o[db]);
+        l += la + lb;
+#if KILN_NEGM
+        mx = max16(sn);
+#else
+        mx = max16(sn) - m;
+#endif
+        sc = sn;
+        st = st1;
+        KILN_FENCE();
+    };
+
+    using True = std::true_type;
+    using False = std::false_type;
+    int j = 0;
+    for (; j < nh - 2; j++) step(False{}, j);
+    if (nh >= 2) {
+        if ((Tk & 31) != 0) step(True{}, j);
+        else step(False{}, j);
+        j++;
+    }
+    // last half tile: no successor
+    if (__builtin_amdgcn_ballot_w64(mx > RESCALE_TH)) {
+        const float d = fmaxf(mx, 0.f);
+        const float corr = __builtin_amdgcn_exp2f(-d);
+#pragma unroll
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[db][i] *= corr;
+        l *= corr;
+        m += d;
+#if KILN_NEGM
+#pragma unroll
+        for (int i = 0; i < 16; i++) sc[i] -= d;
+#endif
+    }
+    {
+#if KILN_NEGM
+        const float mofs = 0.f;
+#else
+        const float mofs = m;
+#endif
+        half8 va[8];
+        const lds_half8* vp = kptr(st) + 32 * HD / 8;
+#pragma unroll
+        for (int g = 0; g < 8; g++) va[g] = vp[g * 64];
+        half8 pb[2];
+#pragma unroll
+        for (int i = 0; i < 16; i++) pb[i / 8][i % 8] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - mofs);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const half2v pr = {pb[t][2 * e], pb[t][2 * e + 1]};
+                l = __builtin_amdgcn_fdot2(pr, ones, l, false);
+            }
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int db = 0; db < 4; db++) o[db] = mfma32(va[t * 4 + db], pb[t], o[db]);
+    }
+    KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is released
+    epilogue<OutT>(p, J, row, qin, W.h, hh, m, l, o);
+#if KILN_CLOCK
+    if (tid == 0 && blockIdx.x < 16384) {
+        g_clk[blockIdx.x][0] = __builtin_amdgcn_s_memtime() - clk0;
+        g_clk[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime() - rt0;
+    }
+#endif
+}
+
 // ------------------------------------------------------------------------------------------------
 // K/V prepare: fp16 conversion (+ K RMSNorm, + K RoPE) into the tiled MFMA operand order.
 // One block per (64-key tile, head). Bandwidth-bound; runs once per K/V, not once per query tile.
@@ -259,7 +494,6 @@ __global__ __launch_bounds__(256) void k_kv_prep(uint16_t* __restrict__ kvp, con
     __shared__ _Float16 vt[KT][HD + 8];
     const int tid = threadIdx.x, j = blockIdx.x, h = blockIdx.y;
     _Float16* dstK = reinterpret_cast<_Float16*>(kvp) + (size_t)h * kv_head_stride(Tk) + (size_t)j * KV_TILE_H;
-    _Float16* dstV = dstK + TILE_H;
 
     const int kk = tid >> 2, qd = tid & 3;  // key within the tile, quarter of the row
     const int key = j * KT + kk;
@@ -312,8 +546,7 @@ __global__ __launch_bounds__(256) void k_kv_prep(uint16_t* __restrict__ kvp, con
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int s = cs[c] >> 1, hb = cs[c] & 1;
-            const int off = ((kb * 8 + s) * 64 + kl + 32 * hb) * 8;
-            *reinterpret_cast<half8*>(dstK + off) = to_half8(x[c]);
+            *reinterpret_cast<half8*>(dstK + kv_k_off(kb, s, kl + 32 * hb)) = to_half8(x[c]);
         }
     }
     // V: tile -> LDS (fp16), then gather the permuted-transposed operand order
@@ -332,15 +565,16 @@ __global__ __launch_bounds__(256) void k_kv_prep(uint16_t* __restrict__ kvp, con
     }
     __syncthreads();
     {
-        const int t = tid >> 6, ln = tid & 63;
-        const int kbase = 16 * t + 4 * (ln >> 5);
+        // unit (c, t, db, lane): 8 keys of one d; thread -> (c, t) = (tid >> 7, (tid >> 6) & 1), 4 db each
+        const int c = tid >> 7, t = (tid >> 6) & 1, ln = tid & 63;
+        const int kbase = 32 * c + 16 * t + 4 * (ln >> 5);
 #pragma unroll
         for (int db = 0; db < 4; db++) {
             const int d = db * 32 + (ln & 31);
             half8 o;
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) o[jj] = vt[kbase + 8 * (jj >> 2) + (jj & 3)][d];
-            *reinterpret_cast<half8*>(dstV + ((db * 4 + t) * 64 + ln) * 8) = o;
+            *reinterpret_cast<half8*>(dstK + kv_v_off(c, t, db, ln)) = o;
         }
     }
 }
@@ -348,14 +582,24 @@ __global__ __launch_bounds__(256) void k_kv_prep(uint16_t* __restrict__ kvp, con
 // ------------------------------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------------------------------
-template <typename InT, typename OutT>
-static hipError_t dispatch_attn(const AttnParams& p, int nblocks, bool qnorm, bool rope, hipStream_t s) {
-    dim3 grid(nblocks), block(NTHR);
-    if (qnorm && rope) hipLaunchKernelGGL((k_attn_fwd<InT, OutT, true, true>), grid, block, 0, s, p);
-    else if (qnorm) hipLaunchKernelGGL((k_attn_fwd<InT, OutT, true, false>), grid, block, 0, s, p);
-    else if (rope) hipLaunchKernelGGL((k_attn_fwd<InT, OutT, false, true>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((k_attn_fwd<InT, OutT, false, false>), grid, block, 0, s, p);
+template <typename InT, typename OutT, bool QN, bool RP>
+static hipError_t launch_sel(AttnParams p, int Tq, int units, hipStream_t s) {
+    p.qtiles = (Tq + BM - 1) / BM;
+    p.total = p.qtiles * units;
+    const int nb = (p.total + 7) / 8 * 8;
+    p.per = nb / 8;
+    auto kern = k_attn_fwd<InT, OutT, QN, RP>;
+    const size_t lds = (size_t)NS * HT_H * sizeof(_Float16);
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(NTHR), lds, s, p);
     return hipGetLastError();
+}
+
+template <typename InT, typename OutT>
+static hipError_t dispatch_attn(const AttnParams& p, int units, bool qnorm, bool rope, hipStream_t s) {
+    if (qnorm && rope) return launch_sel<InT, OutT, true, true>(p, p.Tq, units, s);
+    if (qnorm) return launch_sel<InT, OutT, true, false>(p, p.Tq, units, s);
+    if (rope) return launch_sel<InT, OutT, false, true>(p, p.Tq, units, s);
+    return launch_sel<InT, OutT, false, false>(p, p.Tq, units, s);
 }
 
 hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
@@ -366,10 +610,6 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
     p.H = a.H;
     p.ldq = a.ldq;
     p.ldo = a.ldo;
-    p.qtiles = (a.Tq + BM - 1) / BM;
-    p.total = p.qtiles * a.H * a.njobs;
-    const int nblocks = (p.total + 7) / 8 * 8;
-    p.per = nblocks / 8;
     const size_t osz = a.out == DT::F16 ? 2 : 4;
     bool pairs = (a.ldo * osz) % (4 * osz) != 0;
     for (int i = 0; i < a.njobs; i++) pairs |= ((uintptr_t)a.job[i].o % (4 * osz)) != 0;
@@ -380,13 +620,14 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
     p.rcos = a.rcos;
     p.rsin = a.rsin;
     const bool qn = a.qw != nullptr, rp = a.rcos != nullptr;
-    if (p.total == 0) return hipSuccess;
+    const int units = a.H * a.njobs;
+    if (a.Tq <= 0 || units <= 0) return hipSuccess;
     if (a.in == DT::F16) {
-        if (a.out == DT::F16) return dispatch_attn<_Float16, _Float16>(p, nblocks, qn, rp, s);
-        return dispatch_attn<_Float16, float>(p, nblocks, qn, rp, s);
+        if (a.out == DT::F16) return dispatch_attn<_Float16, _Float16>(p, units, qn, rp, s);
+        return dispatch_attn<_Float16, float>(p, units, qn, rp, s);
     }
-    if (a.out == DT::F16) return dispatch_attn<float, _Float16>(p, nblocks, qn, rp, s);
-    return dispatch_attn<float, float>(p, nblocks, qn, rp, s);
+    if (a.out == DT::F16) return dispatch_attn<float, _Float16>(p, units, qn, rp, s);
+    return dispatch_attn<float, float>(p, units, qn, rp, s);
 }
 
 template <typename InT>
@@ -410,3 +651,9 @@ hipError_t launch_kv_prep(uint16_t* kvp, const void* k, int ldk, const void* v, 
 }
 
 }  // namespace kiln
+
+#if KILN_CLOCK
+extern "C" int kiln_debug_clock(long long* host, int n) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kiln::g_clk), sizeof(long long) * 2 * n);
+}
+#endif

@@ -19,12 +19,18 @@ constexpr int TILE_H = KT * HD;    // halves in one K (or V) tile = 16 KB
 constexpr int KV_TILE_H = 2 * TILE_H;  // K tile followed by V tile, 32 KB
 constexpr float LOG2E = 1.4426950408889634f;
 
-// Prepared K/V buffer of one context: [H][ntiles][K tile | V tile], fp16.
-//  K tile order [kb 2][s 8][lane 64][e 8]:  key = kb*32 + lane%32,  d = 16*s + 8*(lane/32) + e
+// Prepared K/V buffer of one context: [H][ntiles][64-key tile], fp16, zero beyond Tk. A 64-key tile is
+// two 32-key half tiles c = 0, 1, each [K_c 8 KB | V_c 8 KB]:
+//  K_c order [s 8][lane 64][e 8]:  key = 32c + lane%32,  d = 16*s + 8*(lane/32) + e
 //    (lane's 16 bytes are exactly the A operand of v_mfma_f32_32x32x16_f16 for S^T = K Q^T)
-//  V tile order [db 4][t 4][lane 64][j 8]:  d = db*32 + lane%32,
-//    key = 16*t + 8*(j/4) + 4*(lane/32) + j%4
+//  V_c order [t 2][db 4][lane 64][j 8]:  d = db*32 + lane%32,
+//    key = 32c + 16*t + 8*(j/4) + 4*(lane/32) + j%4
 //    (the A operand of O^T = V^T P^T whose B operand P^T is taken straight from the S^T accumulator)
+constexpr int HT_H = 32 * HD * 2;  // halves in one half tile (K_c and V_c), 16 KB
+__host__ __device__ inline int kv_k_off(int c, int s, int lane) { return c * HT_H + (s * 64 + lane) * 8; }
+__host__ __device__ inline int kv_v_off(int c, int t, int db, int lane) {
+    return c * HT_H + 32 * HD + ((t * 4 + db) * 64 + lane) * 8;
+}
 __host__ __device__ inline int kv_tiles(int Tk) { return (Tk + KT - 1) / KT; }
 __host__ __device__ inline size_t kv_head_stride(int Tk) { return (size_t)kv_tiles(Tk) * KV_TILE_H; }
 

@@ -91,8 +91,9 @@ def test_dropin_matches_fp16_semantics_emulator(gpu):
     mx_e, mn_e, _ = errors(got, emu)
     mx_r, mn_r, _ = errors(emu, ref)
     print(f"[parity] kernel vs emulator max {mx_e:.2e} mean {mn_e:.2e}; emulator vs f64 max {mx_r:.2e} mean {mn_r:.2e}")
+    # the kernel must sit closer to the reference's fp16 semantics than those semantics sit to exact math
     assert mn_e <= mn_r, "kernel deviates from the fp16 semantics more than fp16 itself deviates from fp32"
-    assert mx_e <= 1e-3
+    assert mx_e <= mx_r
 
 
 # ---- configs 2 and 4: fused DiT self-attention (QK-RMSNorm + 3D RoPE), CFG batch 2 ----

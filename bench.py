@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fused attention path (one JSON line on stdout).
+
+Headline (`value`): DiT self-attention at 1024x1024 (T = 64x64 = 4096 tokens), CFG batch B=2, H=16, d=128,
+fp16 Q/K/V from random-init linear projections of N(0,1) activations, QK-RMSNorm + Cosmos 3D RoPE fused
+One "step" = one call of the fused path (K/V prepare pass + attention kernel) with
+inputs resident in HBM. FLOP = 4*B*H*Tq*Tk*d (the reference's formula, bench/flash_test.cu:62).
+
+The same line also carries: the S=1536 CFG pair (config 2), the attention ms of a full 28-block DiT step
+at 768x1152 (config 5: self + cross + NAG), the roofline of the dominant kernel (k_attn_fwd, timed alone
+with HIP events on its stream) and the CPU baseline (the reference's fp32 two-pass attention restated in
+C, oracle/oracle.c, on a bounded sample of config 4, on this host's cores).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "attention TFLOP/s + % fp16 MFMA peak at S=1536/4096; ms attn per DiT step"
+PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 flop/clk
+H, D = 16, 128
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_dit_inputs(torch, B, T, seed, dev):
+    """Q/K/V = X W^T (fp16) with X ~ N(0,1) [B*T, 2048], W ~ U(+-1/sqrt(2048)) (torch Linear init)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    X = torch.randn(B * T, H * D, generator=g, device=dev)
+    outs = []
+    for _ in range(3):
+        W = (torch.rand(H * D, H * D, generator=g, device=dev) * 2 - 1) / (H * D) ** 0.5
+        outs.append((X @ W.T).half())
+    del X
+    return outs
+
+
+class Timer:
+    """HIP events on the current stream (the stream every kiln call is enqueued on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+
+def self_attn_case(torch, kiln_amd, Hp, Wp, B, seed, dev):
+    T = Hp * Wp
+    q, k, v = make_dit_inputs(torch, B, T, seed, dev)
+    qw = torch.ones(D, dtype=torch.bfloat16, device=dev)  # torch RMSNorm init
+    kw = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    c, s = kiln_amd.cosmos_rope_tables(Hp, Wp)
+    rope = (c.to(dev), s.to(dev))
+    out = torch.empty_like(q)
+    ws = torch.empty(kiln_amd.dit_self_attn_workspace_bytes(B, T, H), dtype=torch.uint8, device=dev)
+
+    def step():
+        kiln_amd.dit_self_attn(out, q, k, v, B, T, H, qw, kw, rope, workspace=ws)
+
+    # the same work split into its two passes, so the attention kernel can be timed alone
+    kvps = [kiln_amd.kv_prepare(k[b * T:(b + 1) * T], v[b * T:(b + 1) * T], H, k_norm_w=kw, rope=rope)
+            for b in range(B)]
+
+    def main_kernel():
+        kiln_amd.attn_prepped_batch(out, q, kvps, T, T, H, q_norm_w=qw, rope=rope)
+
+    return dict(T=T, B=B, step=step, main=main_kernel, flop=4.0 * B * H * T * T * D, q=q, k=k, v=v, qw=qw, kw=kw,
+                rope=rope)
+
+
+def dit_step_case(torch, kiln_amd, dev, nblocks=28, Hp=48, Wp=72, B=2, L=512, seed=100):
+    """Attention of a full DiT denoising step at 768x1152 (T=3456): per block, self-attention of the CFG pair
+    (QK-norm + RoPE) and cross-attention of each item against its cached context, plus the NAG negative
+    attention of item 0 and the NAG combine (engine/src/dit.cu:458-488). Context K/V are prepared once per
+    generation (Dit::cache_context, engine/src/dit.cu:217-234) and are outside the step."""
+    T = Hp * Wp
+    c, s = kiln_amd.cosmos_rope_tables(Hp, Wp)
+    rope = (c.to(dev), s.to(dev))
+    qw = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    blocks = []
+    ws = torch.empty(kiln_amd.dit_self_attn_workspace_bytes(B, T, H), dtype=torch.uint8, device=dev)
+    for i in range(nblocks):
+        q, k, v = (torch.randn(B * T, H * D, generator=g, device=dev).half() for _ in range(3))
+        qc = torch.randn(B * T, H * D, generator=g, device=dev).half()
+        ctx = []
+        for _ in range(3):  # positive, uncond (CFG item 1), NAG negative
+            kk = torch.randn(L, H * D, generator=g, device=dev).half()
+            vv = torch.randn(L, H * D, generator=g, device=dev).half()
+            ctx.append(kiln_amd.kv_prepare(kk, vv, H, k_norm_w=qw))
+        blocks.append((q, k, v, qc, ctx))
+    a_self = torch.empty(B * T, H * D, dtype=torch.float16, device=dev)
+    a_cross = torch.empty(B * T, H * D, dtype=torch.float16, device=dev)
+    a_neg = torch.empty(T, H * D, dtype=torch.float16, device=dev)
+
+    def step():
+        for q, k, v, qc, ctx in blocks:
+            kiln_amd.dit_self_attn(a_self, q, k, v, B, T, H, qw, qw, rope, workspace=ws)
+            kiln_amd.cross_attn_nag(a_cross, qc, B, T, H, ctx[:2], [L, L], [0, 0], q_norm_w=qw, kvp_neg=ctx[2],
+                                    Lk_neg=L, npad_neg=0, out_neg=a_neg)
+
+    flop = nblocks * (4.0 * B * H * T * T * D + 4.0 * (B + 1) * H * T * L * D)
+    return dict(T=T, step=step, flop=flop)
+
+
+def cpu_baseline(case, target_s=10.0):
+    """The reference's fp32 two-pass attention (bench/flash_test.cu:10-32, restated in oracle/oracle.c) with
+    the QK-RMSNorm and RoPE passes (kernels.cu:656-666, 759-772), on batch item 0 of config 4: the first R
+    query rows against all T keys, R sized to about target_s seconds of CPU work."""
+    import numpy as np
+    import oracle
+    T = case["T"]
+    q = case["q"][:T].float().cpu().numpy()
+    k = case["k"][:T].float().cpu().numpy()
+    v = case["v"][:T].float().cpu().numpy()
+    c = case["rope"][0].cpu().numpy()
+    s = case["rope"][1].cpu().numpy()
+    w = case["qw"].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+    def run(R):
+        t0 = time.perf_counter()
+        qn = oracle.rope_half(oracle.rmsnorm_rows(q[:R], w).reshape(R, H * D), H, c[:R], s[:R])
+        kn = oracle.rope_half(oracle.rmsnorm_rows(k, w).reshape(T, H * D), H, c, s)
+        oracle.ref_attn_f32(qn, kn, v, H)
+        return time.perf_counter() - t0
+
+    t64 = run(64)
+    R = int(min(T, max(64, 64 * target_s / max(t64, 1e-3))) // 64 * 64)
+    dt = run(R)
+    flop = 4.0 * R * H * T * D
+    return dict(value=round(flop / dt / 1e12, 5), unit="TFLOP/s", cores=oracle.num_threads(), kind="port",
+                sample=f"config 4 item 0: {R} of {T} query rows x {H} heads x {T} keys (+ QK-RMSNorm, RoPE), "
+                       f"fp32 two-pass reference attention, {dt:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--main-only", action="store_true",
+                    help="run only the config-4 attention kernel loop (for rocprofv3 runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path has no "
+              f"collective and shards by head with no communication, so run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    import kiln_amd
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    L = kiln_amd.lib()  # fails loudly when the HIP library is missing
+    buf = __import__("ctypes").create_string_buffer(64)
+    L.kiln_attn_device_arch(0, buf, 64)
+    arch = buf.value.decode()
+    tm = Timer(torch)
+
+    cfg4 = self_attn_case(torch, kiln_amd, 64, 64, 2, 4, dev)
+    if args.main_only:
+        ms = tm.run(cfg4["main"], args.steps, args.warmup)
+        log(f"k_attn_fwd config 4: {ms * 1e3:.1f} us  {cfg4['flop'] / ms / 1e9:.1f} TFLOP/s")
+        return 0
+
+    ms4 = tm.run(cfg4["step"], args.steps, args.warmup)
+    ms4_main = tm.run(cfg4["main"], args.steps, args.warmup)
+    tf4 = cfg4["flop"] / ms4 / 1e9
+    tf4_main = cfg4["flop"] / ms4_main / 1e9
+    log(f"config 4 (T=4096, B=2): {ms4 * 1e3:.1f} us/call  {tf4:.1f} TFLOP/s  ({tf4 / PEAK_TFLOPS * 100:.1f}% peak); "
+        f"attention kernel alone {ms4_main * 1e3:.1f} us  {tf4_main:.1f} TFLOP/s")
+
+    cfg2 = self_attn_case(torch, kiln_amd, 32, 48, 2, 2, dev)
+    ms2 = tm.run(cfg2["step"], args.steps, args.warmup)
+    tf2 = cfg2["flop"] / ms2 / 1e9
+    log(f"config 2 (T=1536, B=2): {ms2 * 1e3:.1f} us/call  {tf2:.1f} TFLOP/s  ({tf2 / PEAK_TFLOPS * 100:.1f}% peak)")
+    del cfg2
+
+    cfg5 = dit_step_case(torch, kiln_amd, dev)
+    ms5 = tm.run(cfg5["step"], max(3, args.steps // 4), max(1, args.warmup // 2))
+    log(f"config 5 (T=3456, 28 blocks, self + cross + NAG): {ms5:.3f} ms attention per DiT step  "
+        f"{cfg5['flop'] / ms5 / 1e9:.1f} TFLOP/s")
+    del cfg5
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg4)
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tf4, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms4, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: N(0,1) activations x random-init (torch Linear) projection weights, seeded",
+        "config": {
+            "workload": "config 4: DiT self-attention 1024x1024 (T=4096), CFG batch 2, H=16, d=128, fp16 Q/K/V, "
+                        "QK-RMSNorm + 3D RoPE fused; step = K/V prepare + attention",
+            "arch": arch,
+            "pct_fp16_peak": round(tf4 / PEAK_TFLOPS * 100, 2),
+            "s1536_tflops": round(tf2, 2),
+            "s1536_pct_fp16_peak": round(tf2 / PEAK_TFLOPS * 100, 2),
+            "s1536_ms_per_call": round(ms2, 5),
+            "dit_step_attention_ms": round(ms5, 4),
+            "dit_step_workload": "config 5: 768x1152 (T=3456), B=2, 28 blocks x (self + cross L=512 + NAG)",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "k_attn_fwd",
+            "achieved": round(tf4_main, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tf4_main / PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -106,6 +106,13 @@ int kiln_attn_fwd_prepped(void* out, int out_dtype, int ldo, const void* q, int 
                           const uint16_t* q_norm_w, float eps, const float* rope_cos, const float* rope_sin,
                           const uint16_t* kvp, int Tq, int Tk, int H, int npad, kiln_stream_t stream);
 
+/* Batched form of kiln_attn_fwd_prepped: B independent query sets (q + b*bsq, out + b*bso, elements)
+ * against prepared K/V buffers kvp[b] (host array of B device pointers), one launch. B <= 4. */
+int kiln_attn_fwd_prepped_batch(void* out, int out_dtype, int ldo, long long bso, const void* q, int in_dtype, int ldq,
+                                long long bsq, const uint16_t* q_norm_w, float eps, const float* rope_cos,
+                                const float* rope_sin, const uint16_t* const* kvp, int B, int Tq, int Tk, int H,
+                                int npad, kiln_stream_t stream);
+
 /* Plain batched fp16 attention: B independent (Q, K, V) sets at batch strides bs* (elements). */
 int kiln_attn_fwd_f16in(void* out, int out_dtype, int ldo, long long bso, const uint16_t* q, int ldq, long long bsq,
                         const uint16_t* k, int ldk, long long bsk, const uint16_t* v, int ldv, long long bsv, int B,

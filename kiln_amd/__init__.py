@@ -37,6 +37,8 @@ _SIGS = {
     "kiln_kv_prepped_bytes": (_sz, [_i, _i]),
     "kiln_kv_prepare": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _f, _vp, _vp, _vp]),
     "kiln_attn_fwd_prepped": (_i, [_vp, _i, _i, _vp, _i, _i, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "kiln_attn_fwd_prepped_batch": (_i, [_vp, _i, _i, _ll, _vp, _i, _i, _ll, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i,
+                                         _i, _vp]),
     "kiln_attn_fwd_f16in": (_i, [_vp, _i, _i, _ll, _vp, _i, _ll, _vp, _i, _ll, _vp, _i, _ll, _i, _i, _i, _i, _i,
                                  _vp, _sz, _vp]),
     "kiln_attn_fwd_f16in_workspace_bytes": (_sz, [_i, _i, _i]),
@@ -195,6 +197,17 @@ def attn_prepped(out, q, kvp, Tk, H, npad=0, q_norm_w=None, eps=1e-6, rope=None,
     rc, rs = rope if rope is not None else (None, None)
     _check(lib().kiln_attn_fwd_prepped(_ptr(out), _dt(out), _ld(out), _ptr(q), _dt(q), _ld(q), _bf16_bits(q_norm_w),
                                        eps, _ptr(rc), _ptr(rs), _ptr(kvp), q.shape[0], Tk, H, npad, _stream(stream)))
+    return out
+
+
+def attn_prepped_batch(out, q, kvps, Tq, Tk, H, npad=0, q_norm_w=None, eps=1e-6, rope=None, stream=None):
+    """B query sets (rows b*Tq of q/out) against prepared K/V buffers kvps[b], one launch."""
+    B = len(kvps)
+    rc, rs = rope if rope is not None else (None, None)
+    ptrs = (ctypes.c_void_p * B)(*[k.data_ptr() for k in kvps])
+    _check(lib().kiln_attn_fwd_prepped_batch(_ptr(out), _dt(out), _ld(out), Tq * _ld(out), _ptr(q), _dt(q), _ld(q),
+                                             Tq * _ld(q), _bf16_bits(q_norm_w), eps, _ptr(rc), _ptr(rs),
+                                             ctypes.cast(ptrs, _vp), B, Tq, Tk, H, npad, _stream(stream)))
     return out
 
 

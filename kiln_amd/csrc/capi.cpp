@@ -205,6 +205,41 @@ int kiln_attn_fwd_prepped(void* out, int out_dtype, int ldo, const void* q, int 
     return hip_check(kiln::launch_attn_fwd(a, (hipStream_t)stream), "attn_fwd launch");
 }
 
+int kiln_attn_fwd_prepped_batch(void* out, int out_dtype, int ldo, long long bso, const void* q, int in_dtype, int ldq,
+                                long long bsq, const uint16_t* q_norm_w, float eps, const float* rope_cos,
+                                const float* rope_sin, const uint16_t* const* kvp, int B, int Tq, int Tk, int H,
+                                int npad, kiln_stream_t stream) {
+    if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
+        return fail(KILN_EINVAL, "dtype");
+    int r = check_common(Tq, Tk, H, npad);
+    if (r) return r;
+    if (B <= 0 || B > kiln::MAX_JOBS) return fail(KILN_EUNSUPPORTED, "batch %d outside 1..%d", B, kiln::MAX_JOBS);
+    if (Tq == 0) return KILN_OK;
+    if (Tk == 0) return fail(KILN_EUNSUPPORTED, "batched prepped attention needs Tk > 0");
+    if (!out || !q || !kvp) return fail(KILN_EINVAL, "null pointer");
+    const DT in = (DT)in_dtype, od = (DT)out_dtype;
+    const size_t isz = in == DT::F16 ? 2 : 4, osz = od == DT::F16 ? 2 : 4;
+    if (!rows_ok(q, ldq, in) || ldo % 2 || (bsq * (long long)isz) % 16) return fail(KILN_EUNSUPPORTED, "Q rows not 16-byte aligned");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(KILN_EINVAL, "rope tables: need both cos and sin");
+    kiln::AttnLaunch a{};
+    for (int b = 0; b < B; b++) {
+        if (!kvp[b] || !aligned16(kvp[b])) return fail(KILN_EINVAL, "kvp[%d] null or misaligned", b);
+        a.job[b] = {(const char*)q + bsq * b * isz, kvp[b], (char*)out + bso * b * osz, Tk, npad};
+    }
+    a.njobs = B;
+    a.Tq = Tq;
+    a.H = H;
+    a.ldq = ldq;
+    a.ldo = ldo;
+    a.in = in;
+    a.out = od;
+    a.qw = q_norm_w;
+    a.eps = eps;
+    a.rcos = rope_cos;
+    a.rsin = rope_sin;
+    return hip_check(kiln::launch_attn_fwd(a, (hipStream_t)stream), "attn_fwd launch");
+}
+
 int kiln_attn_fwd_f32out(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                          int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream) {
     int r = check_common(Tq, Tk, H, npad);

@@ -1,0 +1,88 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/kiln_attn.h declares, and its
+host-side logic (status strings, argument validation that returns before any HIP call, buffer sizes, the
+host Cosmos RoPE tables) behaves as documented. No kernel is launched here."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import kiln_amd
+import oracle
+
+
+@pytest.fixture(scope="module")
+def L():
+    return kiln_amd.lib()
+
+
+def test_exports_every_header_symbol(L):
+    syms = kiln_amd.header_symbols()
+    assert len(syms) >= 18
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, f"declared in include/kiln_attn.h but not exported: {missing}"
+    # every declared symbol is bound with a signature in the Python mirror, and nothing else is
+    assert sorted(kiln_amd._SIGS) == syms
+
+
+def test_status_strings(L):
+    for code in range(5):
+        assert L.kiln_attn_status_string(code).decode()
+    assert L.kiln_attn_status_string(99).decode() == "unknown status"
+
+
+def test_kv_prepped_bytes(L):
+    # [H][ceil(Tk/64)][K 16 KB | V 16 KB]
+    assert L.kiln_kv_prepped_bytes(1, 16) == 16 * 1 * 32768
+    assert L.kiln_kv_prepped_bytes(64, 16) == 16 * 1 * 32768
+    assert L.kiln_kv_prepped_bytes(65, 2) == 2 * 2 * 32768
+    assert L.kiln_kv_prepped_bytes(4096, 16) == 16 * 64 * 32768
+    assert L.kiln_kv_prepped_bytes(0, 16) == 0
+    assert L.kiln_dit_self_attn_workspace_bytes(2, 4096, 16) == 2 * L.kiln_kv_prepped_bytes(4096, 16)
+
+
+def test_cosmos_rope_tables_host_equal_oracle(L):
+    """kiln_cosmos_rope_tables is host code in the library (engine/src/dit.cu:196-215): bitwise equal to the
+    oracle's restatement, which tests/test_oracle.py pins against the float64 Cosmos formulas."""
+    for Hp, Wp in ((32, 48), (64, 64), (48, 72)):
+        c = np.empty((Hp * Wp, 64), np.float32)
+        s = np.empty((Hp * Wp, 64), np.float32)
+        assert L.kiln_cosmos_rope_tables(c.ctypes.data, s.ctypes.data, Hp, Wp) == 0
+        oc, os_ = oracle.cosmos_rope(Hp, Wp)
+        np.testing.assert_array_equal(c, oc)
+        np.testing.assert_array_equal(s, os_)
+    assert L.kiln_cosmos_rope_tables(None, None, 4, 4) == kiln_amd.KILN_EINVAL
+
+
+def test_argument_validation_without_gpu(L):
+    """Checks that reject a call before any HIP call (the reference throws on the same shapes)."""
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+    # attention16 needs Dh = 128 (engine/src/kernels.cu:870)
+    assert L.kiln_attn_fwd_f16out(p, 1024, p, 1024, p, 1024, p, 1024, 8, 8, 16, 64, 0, None) == kiln_amd.KILN_EUNSUPPORTED
+    assert "head size" in L.kiln_attn_last_error().decode()
+    # no keys at all: softmax undefined
+    assert L.kiln_attn_fwd_f32out(p, 2048, p, 2048, p, 2048, p, 2048, 8, 0, 16, 128, 0, 0, None) == kiln_amd.KILN_EINVAL
+    # negative sizes
+    assert L.kiln_attn_fwd_f32out(p, 2048, p, 2048, p, 2048, p, 2048, -1, 8, 16, 128, 0, 0, None) == kiln_amd.KILN_EINVAL
+    # exact path: head size bound
+    assert L.kiln_attn_fwd_exact(p, 4096, p, 4096, p, 4096, p, 4096, 8, 8, 8, 512, 0, 0, None) == kiln_amd.KILN_EUNSUPPORTED
+    # dtype codes
+    assert L.kiln_nag_combine(p, 8, p, 8, 7, 4, 8, 5.0, 2.5, 0.25, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_kv_prepare(p, p, 2048, p, 2048, 3, 64, 16, None, 1e-6, None, None, None) == kiln_amd.KILN_EINVAL
+    # more batch items than one launch takes
+    assert L.kiln_dit_self_attn_fused(p, 1, 2048, p, p, p, 1, 2048, None, None, 1e-6, None, None, 5, 64, 16, None, 0,
+                                      None) != kiln_amd.KILN_OK
+
+
+def test_python_wrappers_raise_kiln_error(L):
+    with pytest.raises(kiln_amd.KilnError) as e:
+        kiln_amd._check(kiln_amd.KILN_EUNSUPPORTED)
+    assert e.value.status == kiln_amd.KILN_EUNSUPPORTED
+
+
+def test_cpp_host_header_compiles():
+    """kiln_amd/host/kiln_gpu.hpp (the reference-named C++ mirror) compiles against the C ABI header."""
+    import subprocess
+    src = '#include "kiln_amd/host/kiln_gpu.hpp"\nint main() { kiln::set_stream(nullptr); return 0; }\n'
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-fsyntax-only", "-x", "hip", "-", "-I", kiln_amd.os.path.dirname(kiln_amd._HERE)],
+                       input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

@@ -161,6 +161,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--main-only", action="store_true",
                     help="run only the config-4 attention kernel loop (for rocprofv3 runs)")
+    ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
+                    help="copy a MIB-sized device buffer --steps times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path has no "
@@ -179,6 +181,12 @@ def main():
     L.kiln_attn_device_arch(0, buf, 64)
     arch = buf.value.decode()
     tm = Timer(torch)
+    if args.copy_cal:
+        src = torch.empty(args.copy_cal << 18, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        ms = tm.run(lambda: dst.copy_(src), args.steps, args.warmup)
+        log(f"copy {args.copy_cal} MiB: {ms * 1e3:.1f} us  {2 * src.numel() * 4 / ms / 1e6:.1f} GB/s")
+        return 0
 
     cfg4 = self_attn_case(torch, kiln_amd, 64, 64, 2, 4, dev)
     if args.main_only:
@@ -204,6 +212,12 @@ def main():
     log(f"config 5 (T=3456, 28 blocks, self + cross + NAG): {ms5:.3f} ms attention per DiT step  "
         f"{cfg5['flop'] / ms5 / 1e9:.1f} TFLOP/s")
     del cfg5
+
+    traffic = None  # HBM bytes per launch of k_attn_fwd (config 4), from the committed rocprofv3 FETCH/WRITE runs
+    tpath = os.path.join(ROOT, "profiles", "k_attn_fwd_config4_hbm_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("traffic_bytes")
 
     cpu = None
     if not args.no_cpu:
@@ -241,7 +255,7 @@ def main():
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tf4_main / PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
         "cpu_baseline": cpu,
     }

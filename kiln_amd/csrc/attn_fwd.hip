@@ -219,20 +219,33 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 #else
 #define KILN_FENCE() ((void)0)
 #endif
+#ifndef KILN_PRIO
+#define KILN_PRIO 0
+#endif
+#ifndef KILN_QSPLIT
+#define KILN_QSPLIT 0
+#endif
 #ifndef KILN_NEGM
 #define KILN_NEGM 0
 #endif
 typedef __attribute__((address_space(3))) half8 lds_half8;
-constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = KILN_NS;
+#ifndef KILN_NW
+#define KILN_NW 4
+#endif
+constexpr int NW = KILN_NW, NTHR = NW * 64, BM = NW * 32, NS = KILN_NS;
 constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile (4)
 static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
 
 #if KILN_CLOCK
 __device__ long long g_clk[16384][2];  // per workgroup: shader cycles, 100 MHz ticks (debug builds only)
+__device__ long long g_phase[16384][4];  // per workgroup (wave 0): cycles in the 4 phases of the steps
+#define KILN_T(var) const long long var = __builtin_amdgcn_s_memtime()
+#else
+#define KILN_T(var) ((void)0)
 #endif
 
 template <typename InT, typename OutT, bool QNORM, bool ROPE>
-__global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
+__global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
 #if KILN_CLOCK
     const long long clk0 = __builtin_amdgcn_s_memtime(), rt0 = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -320,7 +333,14 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
     float mx = 0.f;  // max(S_j) - m
 #pragma unroll
     for (int s = 0; s < 4; s++) ka[s] = kptr(1 % NS)[s * 64];
+    // Enter the loop with no LDS read in flight: the loop body's first MFMA then waits only for the reads
+    // of the previous iteration, and the waitcnt pass can keep the step's own 8 new reads in flight
+    // (otherwise it merges the two entry states and waits for everything before the first QK MFMA).
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 
+#if KILN_CLOCK
+    long long ph[4] = {0, 0, 0, 0};
+#endif
     int st = 0;            // stage of half tile j
     int st2 = NS - 1;      // stage that receives half tile j+NS-1
     // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
@@ -330,6 +350,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
     // K_{j+1}[4,8) reads are consumed (waited on) before the next iteration's barrier.
     auto step = [&](auto maskn_tag, int j) {
         constexpr bool MASKN = decltype(maskn_tag)::value;
+        KILN_T(t0);
         if (__builtin_amdgcn_ballot_w64(mx > RESCALE_TH)) {  // lazy rescale (rare)
             const float d = fmaxf(mx, 0.f);
             const float corr = __builtin_amdgcn_exp2f(-d);
@@ -363,18 +384,32 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
             for (int g = 0; g < 4; g++) va[g] = vp[g * 64];
         }
         KILN_FENCE();
+        KILN_T(t1);
 
         // S_{j+1} on the matrix core while the VALU turns S_j into P_j
+#if KILN_PRIO
+        __builtin_amdgcn_s_setprio(1);
+#endif
 #if KILN_NEGM
         floatx16 sn = mfma32(ka[0], qreg[0], negm);
 #else
         floatx16 sn = mfma32(ka[0], qreg[0], floatx16{});
 #endif
+#if KILN_QSPLIT
+        floatx16 sn2 = mfma32(ka[1], qreg[1], floatx16{});
+#endif
         half8 pb[2];
         float la = 0.f, lb = 0.f;
 #pragma unroll
         for (int s = 0; s < 8; s++) {
+#if KILN_QSPLIT
+            if (s > 1) {
+                if (s & 1) sn2 = mfma32(ka[s], qreg[s], sn2);
+                else sn = mfma32(ka[s], qreg[s], sn);
+            }
+#else
             if (s > 0) sn = mfma32(ka[s], qreg[s], sn);
+#endif
             const float e0 = __builtin_amdgcn_exp2f(sc[2 * s] - mofs);
             const float e1 = __builtin_amdgcn_exp2f(sc[2 * s + 1] - mofs);
             pb[s / 4][(2 * s) % 8] = (_Float16)e0;
@@ -386,7 +421,14 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
                 lb = __builtin_amdgcn_fdot2(p1, ones, lb, false);
             }
         }
+#if KILN_PRIO
+        __builtin_amdgcn_s_setprio(0);
+#endif
+#if KILN_QSPLIT
+        sn += sn2;
+#endif
         KILN_FENCE();
+        KILN_T(t2);
 
         // tile j+2 landed in every wave; every wave is done with tile j-1
         // only tiles j+3 .. j+NS-2 may be in flight; the peeled masking step (whose register spills are
@@ -394,6 +436,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
         if constexpr (MASKN) KILN_WAIT_VMCNT(0);
         else KILN_WAIT_VMCNT((NS - 4) * DMA_PER_HT);
         __builtin_amdgcn_s_barrier();
+        KILN_T(t3);
         dma(min(j + NS - 1, nh - 1), st2);  // into the stage of tile j-1
         st2 = st2 == NS - 1 ? 0 : st2 + 1;
         half8 vb[4];
@@ -408,10 +451,16 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
         KILN_FENCE();
 
         if constexpr (MASKN) mask_half(j + 1, Tk, hh, sn);
+#if KILN_PRIO
+        __builtin_amdgcn_s_setprio(1);
+#endif
 #pragma unroll
         for (int db = 0; db < 4; db++) o[db] = mfma32(va[db], pb[0], o[db]);
 #pragma unroll
         for (int db = 0; db < 4; db++) o[db] = mfma32(vb[db], pb[1], o[db]);
+#if KILN_PRIO
+        __builtin_amdgcn_s_setprio(0);
+#endif
         l += la + lb;
 #if KILN_NEGM
         mx = max16(sn);
@@ -421,6 +470,13 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
         sc = sn;
         st = st1;
         KILN_FENCE();
+#if KILN_CLOCK
+        KILN_T(t4);
+        ph[0] += t1 - t0;
+        ph[1] += t2 - t1;
+        ph[2] += t3 - t2;
+        ph[3] += t4 - t3;
+#endif
     };
 
     using True = std::true_type;
@@ -478,6 +534,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {
     if (tid == 0 && blockIdx.x < 16384) {
         g_clk[blockIdx.x][0] = __builtin_amdgcn_s_memtime() - clk0;
         g_clk[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime() - rt0;
+        for (int i = 0; i < 4; i++) g_phase[blockIdx.x][i] = ph[i];
     }
 #endif
 }
@@ -655,5 +712,8 @@ hipError_t launch_kv_prep(uint16_t* kvp, const void* k, int ldk, const void* v, 
 #if KILN_CLOCK
 extern "C" int kiln_debug_clock(long long* host, int n) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kiln::g_clk), sizeof(long long) * 2 * n);
+}
+extern "C" int kiln_debug_phase(long long* host, int n) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kiln::g_phase), sizeof(long long) * 4 * n);
 }
 #endif

@@ -28,9 +28,6 @@
 namespace kiln {
 
 constexpr float RESCALE_TH = 8.0f;
-#ifndef KILN_SCHED
-#define KILN_SCHED 0
-#endif
 
 struct AttnParams {
     AttnJob job[MAX_JOBS];
@@ -192,60 +189,53 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 #define KILN_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (0xF << 8) | (((N) >> 4) << 14))
 
 // ------------------------------------------------------------------------------------------------
-// The kernel: 4 waves x 32 query rows (BM = 128) per workgroup, two workgroups per CU (2 waves per
-// SIMD, from independent workgroups). Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB)
-// through an NS-stage LDS ring filled by direct global->LDS DMA (global_load_lds_dwordx4: no staging
-// registers, no ds_write), NS-1 half tiles ahead of use.
+// The kernel. A wave owns QB query blocks of 32 rows (QB = 2: 64 rows), a workgroup NW waves
+// (BM = NW * QB * 32 rows, 128 by default), two workgroups per CU. With QB = 2 each wave has two
+// independent MFMA dependency chains per phase, K/V operand reads, the DMA and the barrier are shared by
+// both blocks, and the register budget (one wave per SIMD) lets the compiler keep the O accumulators in
+// AGPRs, where the matrix cores update them without competing with the VALU for VGPR ports.
 //
-// Scores are kept relative to the running max m: each QK^T MFMA chain starts from C = -m, so S - m
-// comes out of the matrix core and p = 2^(S - m) needs one v_exp per score.
+// Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB) through an NS-stage LDS ring filled by
+// direct global->LDS DMA (global_load_lds_dwordx4: no staging registers, no ds_write), NS-2 half tiles
+// ahead of use.
 //
-// Software pipeline, per half tile j (S_j - m and max(S_j) in registers, K_{j+1} operands in
-// registers, half tiles j .. j+NS-2 resident or in flight):
+// Software pipeline, per half tile j (S_j and max(S_j) - m in registers, K_{j+1}[0,4) operands in
+// registers, half tiles j .. j+NS-3 resident or in flight):
 //   [rare: rescale O, l, m]                                         (the only branch)
-//   V_j reads | DMA tile j+NS-1 | QK_{j+1} MFMAs interleaved with exp/cvt/row-sum of S_j |
-//   wait tile j+2, barrier | K_{j+2} reads | PV_j MFMAs interleaved with max(S_{j+1})
-// so each wave always has an independent MFMA chain in flight under its VALU work, and every LDS
-// read is issued one phase before its use.
+//   K_{j+1}[4,8), V_j[t=0] reads | QK_{j+1} MFMAs interleaved with exp/cvt/row-sum of S_j |
+//   wait tile j+2, barrier | DMA tile j+NS-1 into the stage of tile j-1 | K_{j+2}[0,4), V_j[t=1] reads |
+//   PV_j MFMAs interleaved with max(S_{j+1})
+// Every read of a stage completes before the barrier that precedes its refill.
 // ------------------------------------------------------------------------------------------------
 #ifndef KILN_NS
 #define KILN_NS 5
 #endif
-#ifndef KILN_PIN
-#define KILN_PIN 1
+#ifndef KILN_QB
+#define KILN_QB 1
 #endif
-#if KILN_PIN
+#ifndef KILN_NW
+#define KILN_NW (4 / KILN_QB)
+#endif
+#ifndef KILN_FENCES
+#define KILN_FENCES 1
+#endif
+#if KILN_FENCES
 #define KILN_FENCE() __builtin_amdgcn_sched_barrier(0)
 #else
 #define KILN_FENCE() ((void)0)
 #endif
-#ifndef KILN_PRIO
-#define KILN_PRIO 0
-#endif
-#ifndef KILN_QSPLIT
-#define KILN_QSPLIT 0
-#endif
-#ifndef KILN_NEGM
-#define KILN_NEGM 0
-#endif
 typedef __attribute__((address_space(3))) half8 lds_half8;
-#ifndef KILN_NW
-#define KILN_NW 4
-#endif
-constexpr int NW = KILN_NW, NTHR = NW * 64, BM = NW * 32, NS = KILN_NS;
-constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile (4)
+constexpr int QB = KILN_QB, NW = KILN_NW, NTHR = NW * 64, BM = NW * QB * 32, NS = KILN_NS;
+constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
 static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
+static_assert(NW * QB == 4, "two workgroups of four 32-row blocks per CU");
 
 #if KILN_CLOCK
 __device__ long long g_clk[16384][2];  // per workgroup: shader cycles, 100 MHz ticks (debug builds only)
-__device__ long long g_phase[16384][4];  // per workgroup (wave 0): cycles in the 4 phases of the steps
-#define KILN_T(var) const long long var = __builtin_amdgcn_s_memtime()
-#else
-#define KILN_T(var) ((void)0)
 #endif
 
 template <typename InT, typename OutT, bool QNORM, bool ROPE>
-__global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
+__global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {  // 2nd: waves per SIMD
 #if KILN_CLOCK
     const long long clk0 = __builtin_amdgcn_s_memtime(), rt0 = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -257,10 +247,15 @@ __global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
     if (!decode_work(p, W)) return;
     const AttnJob J = p.job[W.jb];
 
-    const int row = W.qt * BM + wv * 32 + (lane & 31);
-    const bool qin = row < p.Tq;
-    half8 qreg[8];
-    load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, hh, qreg);
+    int row[QB];
+    bool qin[QB];
+    half8 qreg[QB][8];
+#pragma unroll
+    for (int b = 0; b < QB; b++) {
+        row[b] = W.qt * BM + (wv * QB + b) * 32 + (lane & 31);
+        qin[b] = row[b] < p.Tq;
+        load_q<InT, QNORM, ROPE>(p, J.q, row[b], qin[b], W.h, hh, qreg[b]);
+    }
 
     const int Tk = J.Tk;
     const int nh = (Tk + 31) / 32;  // half tiles holding real keys
@@ -281,16 +276,6 @@ __global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
     auto kptr = [&](int stage) {
         return reinterpret_cast<const lds_half8*>((size_t)(lds_base + stage * HT_H * 2 + lane * 16));
     };
-    auto read_k = [&](int stage, half8 (&ka)[8]) {
-        const lds_half8* kp = kptr(stage);
-#pragma unroll
-        for (int s = 0; s < 8; s++) ka[s] = kp[s * 64];
-    };
-    auto read_v = [&](int stage, half8 (&va)[8]) {
-        const lds_half8* vp = kptr(stage) + 32 * HD / 8;
-#pragma unroll
-        for (int g = 0; g < 8; g++) va[g] = vp[g * 64];
-    };
     auto max16 = [](const floatx16& a) {
         const float x0 = fmaxf(fmaxf(a[0], a[1]), a[2]), x1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
         const float x2 = fmaxf(fmaxf(a[6], a[7]), a[8]), x3 = fmaxf(fmaxf(a[9], a[10]), a[11]);
@@ -304,75 +289,64 @@ __global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
     KILN_WAIT_VMCNT((NS - 3) * DMA_PER_HT);
     __builtin_amdgcn_s_barrier();
 
-    floatx16 o[4];
+    floatx16 o[QB][4];
+    float m[QB], l[QB], mx[QB];
+    floatx16 sc[QB];  // S_j
 #pragma unroll
-    for (int db = 0; db < 4; db++)
+    for (int b = 0; b < QB; b++) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) o[db][i] = 0.f;
-    float l = 0.f;
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[b][db][i] = 0.f;
+        l[b] = 0.f;
+    }
     const half2v ones = {(_Float16)1.f, (_Float16)1.f};
 
-    half8 ka[8];  // K operands: [0,4) of the next QK chain are read a phase ahead of [4,8)
+    half8 ka[8];  // K operands: [0,4) of the next QK chains are read a phase ahead of [4,8)
 #pragma unroll
     for (int s = 0; s < 8; s++) ka[s] = kptr(0)[s * 64];
-    floatx16 sc;  // S_j (relative to m when KILN_NEGM)
 #pragma unroll
-    for (int i = 0; i < 16; i++) sc[i] = 0.f;
+    for (int b = 0; b < QB; b++) {
 #pragma unroll
-    for (int s = 0; s < 8; s++) sc = mfma32(ka[s], qreg[s], sc);
-    if (Tk < 32) mask_half(0, Tk, hh, sc);
-    float m = max16(sc);  // the first half tile sets the running max
-#if KILN_NEGM
-    floatx16 negm;  // -m in every accumulator slot: the C operand that starts each QK^T chain
+        for (int i = 0; i < 16; i++) sc[b][i] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        sc[i] -= m;
-        negm[i] = -m;
+        for (int s = 0; s < 8; s++) sc[b] = mfma32(ka[s], qreg[b][s], sc[b]);
+        if (Tk < 32) mask_half(0, Tk, hh, sc[b]);
+        m[b] = max16(sc[b]);  // the first half tile sets the running max
+        mx[b] = 0.f;          // max(S_j) - m
     }
-#endif
-    float mx = 0.f;  // max(S_j) - m
 #pragma unroll
     for (int s = 0; s < 4; s++) ka[s] = kptr(1 % NS)[s * 64];
     // Enter the loop with no LDS read in flight: the loop body's first MFMA then waits only for the reads
-    // of the previous iteration, and the waitcnt pass can keep the step's own 8 new reads in flight
-    // (otherwise it merges the two entry states and waits for everything before the first QK MFMA).
+    // of the previous iteration, and the waitcnt pass keeps the step's own new reads in flight.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 
-#if KILN_CLOCK
-    long long ph[4] = {0, 0, 0, 0};
-#endif
-    int st = 0;            // stage of half tile j
-    int st2 = NS - 1;      // stage that receives half tile j+NS-1
+    auto rescale = [&](int b) {
+        const float d = fmaxf(mx[b], 0.f);
+        const float corr = __builtin_amdgcn_exp2f(-d);
+#pragma unroll
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[b][db][i] *= corr;
+        l[b] *= corr;
+        m[b] += d;
+    };
+    auto need_rescale = [&]() {
+        bool need = false;
+#pragma unroll
+        for (int b = 0; b < QB; b++) need |= mx[b] > RESCALE_TH;
+        return __builtin_amdgcn_ballot_w64(need) != 0;
+    };
+
+    int st = 0;        // stage of half tile j
+    int st2 = NS - 1;  // stage that receives half tile j+NS-1
     // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
-    //   rescale (rare) | K_{j+1}[4,8), V_j[t=0] reads | QK_{j+1} || exp S_j | wait tile j+2, barrier |
-    //   DMA tile j+NS-1 into the stage of tile j-1 | K_{j+2}[0,4), V_j[t=1] reads | PV_j || max S_{j+1}
-    // Every read of a stage completes before the barrier that precedes its refill: V_j[t=1] and the
-    // K_{j+1}[4,8) reads are consumed (waited on) before the next iteration's barrier.
     auto step = [&](auto maskn_tag, int j) {
         constexpr bool MASKN = decltype(maskn_tag)::value;
-        KILN_T(t0);
-        if (__builtin_amdgcn_ballot_w64(mx > RESCALE_TH)) {  // lazy rescale (rare)
-            const float d = fmaxf(mx, 0.f);
-            const float corr = __builtin_amdgcn_exp2f(-d);
+        if (need_rescale()) {  // lazy rescale (rare)
 #pragma unroll
-            for (int db = 0; db < 4; db++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) o[db][i] *= corr;
-            l *= corr;
-            m += d;
-#if KILN_NEGM
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                sc[i] -= d;
-                negm[i] = -m;
-            }
-#endif
+            for (int b = 0; b < QB; b++) rescale(b);
         }
-#if KILN_NEGM
-        const float mofs = 0.f;  // sc already holds S - m
-#else
-        const float mofs = m;
-#endif
         const int st1 = st == NS - 1 ? 0 : st + 1;
         half8 va[4];
         {
@@ -384,59 +358,40 @@ __global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
             for (int g = 0; g < 4; g++) va[g] = vp[g * 64];
         }
         KILN_FENCE();
-        KILN_T(t1);
 
-        // S_{j+1} on the matrix core while the VALU turns S_j into P_j
-#if KILN_PRIO
-        __builtin_amdgcn_s_setprio(1);
-#endif
-#if KILN_NEGM
-        floatx16 sn = mfma32(ka[0], qreg[0], negm);
-#else
-        floatx16 sn = mfma32(ka[0], qreg[0], floatx16{});
-#endif
-#if KILN_QSPLIT
-        floatx16 sn2 = mfma32(ka[1], qreg[1], floatx16{});
-#endif
-        half8 pb[2];
-        float la = 0.f, lb = 0.f;
+        // S_{j+1} on the matrix cores while the VALU turns S_j into P_j
+        floatx16 sn[QB];
+#pragma unroll
+        for (int b = 0; b < QB; b++) sn[b] = mfma32(ka[0], qreg[b][0], floatx16{});
+        half8 pb[QB][2];
+        float la[QB], lb[QB];
+#pragma unroll
+        for (int b = 0; b < QB; b++) la[b] = lb[b] = 0.f;
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-#if KILN_QSPLIT
-            if (s > 1) {
-                if (s & 1) sn2 = mfma32(ka[s], qreg[s], sn2);
-                else sn = mfma32(ka[s], qreg[s], sn);
-            }
-#else
-            if (s > 0) sn = mfma32(ka[s], qreg[s], sn);
-#endif
-            const float e0 = __builtin_amdgcn_exp2f(sc[2 * s] - mofs);
-            const float e1 = __builtin_amdgcn_exp2f(sc[2 * s + 1] - mofs);
-            pb[s / 4][(2 * s) % 8] = (_Float16)e0;
-            pb[s / 4][(2 * s + 1) % 8] = (_Float16)e1;
-            if (s & 1) {  // row sum of the fp16-rounded P values the PV MFMA consumes
-                const half2v p0 = {pb[s / 4][(2 * s - 2) % 8], pb[s / 4][(2 * s - 1) % 8]};
-                const half2v p1 = {pb[s / 4][(2 * s) % 8], pb[s / 4][(2 * s + 1) % 8]};
-                la = __builtin_amdgcn_fdot2(p0, ones, la, false);
-                lb = __builtin_amdgcn_fdot2(p1, ones, lb, false);
+#pragma unroll
+            for (int b = 0; b < QB; b++) {
+                if (s > 0) sn[b] = mfma32(ka[s], qreg[b][s], sn[b]);
+                const float e0 = __builtin_amdgcn_exp2f(sc[b][2 * s] - m[b]);
+                const float e1 = __builtin_amdgcn_exp2f(sc[b][2 * s + 1] - m[b]);
+                pb[b][s / 4][(2 * s) % 8] = (_Float16)e0;
+                pb[b][s / 4][(2 * s + 1) % 8] = (_Float16)e1;
+                if (s & 1) {  // row sum of the fp16-rounded P values the PV MFMA consumes
+                    const half2v p0 = {pb[b][s / 4][(2 * s - 2) % 8], pb[b][s / 4][(2 * s - 1) % 8]};
+                    const half2v p1 = {pb[b][s / 4][(2 * s) % 8], pb[b][s / 4][(2 * s + 1) % 8]};
+                    la[b] = __builtin_amdgcn_fdot2(p0, ones, la[b], false);
+                    lb[b] = __builtin_amdgcn_fdot2(p1, ones, lb[b], false);
+                }
             }
         }
-#if KILN_PRIO
-        __builtin_amdgcn_s_setprio(0);
-#endif
-#if KILN_QSPLIT
-        sn += sn2;
-#endif
         KILN_FENCE();
-        KILN_T(t2);
 
-        // tile j+2 landed in every wave; every wave is done with tile j-1
-        // only tiles j+3 .. j+NS-2 may be in flight; the peeled masking step (whose register spills are
-        // vector memory operations too) waits for everything
+        // tile j+2 landed in every wave; every wave is done with tile j-1. Only tiles j+3 .. j+NS-2 may be
+        // in flight; the peeled masking step (whose register spills, if any, are vector memory operations
+        // too) waits for everything.
         if constexpr (MASKN) KILN_WAIT_VMCNT(0);
         else KILN_WAIT_VMCNT((NS - 4) * DMA_PER_HT);
         __builtin_amdgcn_s_barrier();
-        KILN_T(t3);
         dma(min(j + NS - 1, nh - 1), st2);  // into the stage of tile j-1
         st2 = st2 == NS - 1 ? 0 : st2 + 1;
         half8 vb[4];
@@ -450,33 +405,25 @@ __global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
         }
         KILN_FENCE();
 
-        if constexpr (MASKN) mask_half(j + 1, Tk, hh, sn);
-#if KILN_PRIO
-        __builtin_amdgcn_s_setprio(1);
-#endif
 #pragma unroll
-        for (int db = 0; db < 4; db++) o[db] = mfma32(va[db], pb[0], o[db]);
+        for (int b = 0; b < QB; b++)
+            if constexpr (MASKN) mask_half(j + 1, Tk, hh, sn[b]);
 #pragma unroll
-        for (int db = 0; db < 4; db++) o[db] = mfma32(vb[db], pb[1], o[db]);
-#if KILN_PRIO
-        __builtin_amdgcn_s_setprio(0);
-#endif
-        l += la + lb;
-#if KILN_NEGM
-        mx = max16(sn);
-#else
-        mx = max16(sn) - m;
-#endif
-        sc = sn;
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int b = 0; b < QB; b++) o[b][db] = mfma32(va[db], pb[b][0], o[b][db]);
+#pragma unroll
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int b = 0; b < QB; b++) o[b][db] = mfma32(vb[db], pb[b][1], o[b][db]);
+#pragma unroll
+        for (int b = 0; b < QB; b++) {
+            l[b] += la[b] + lb[b];
+            mx[b] = max16(sn[b]) - m[b];
+            sc[b] = sn[b];
+        }
         st = st1;
         KILN_FENCE();
-#if KILN_CLOCK
-        KILN_T(t4);
-        ph[0] += t1 - t0;
-        ph[1] += t2 - t1;
-        ph[2] += t3 - t2;
-        ph[3] += t4 - t3;
-#endif
     };
 
     using True = std::true_type;
@@ -489,52 +436,40 @@ __global__ __launch_bounds__(NTHR, 8 / NW) void k_attn_fwd(const AttnParams p) {
         j++;
     }
     // last half tile: no successor
-    if (__builtin_amdgcn_ballot_w64(mx > RESCALE_TH)) {
-        const float d = fmaxf(mx, 0.f);
-        const float corr = __builtin_amdgcn_exp2f(-d);
+    if (need_rescale()) {
 #pragma unroll
-        for (int db = 0; db < 4; db++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[db][i] *= corr;
-        l *= corr;
-        m += d;
-#if KILN_NEGM
-#pragma unroll
-        for (int i = 0; i < 16; i++) sc[i] -= d;
-#endif
+        for (int b = 0; b < QB; b++) rescale(b);
     }
     {
-#if KILN_NEGM
-        const float mofs = 0.f;
-#else
-        const float mofs = m;
-#endif
         half8 va[8];
         const lds_half8* vp = kptr(st) + 32 * HD / 8;
 #pragma unroll
         for (int g = 0; g < 8; g++) va[g] = vp[g * 64];
-        half8 pb[2];
 #pragma unroll
-        for (int i = 0; i < 16; i++) pb[i / 8][i % 8] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - mofs);
+        for (int b = 0; b < QB; b++) {
+            half8 pb[2];
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+            for (int i = 0; i < 16; i++) pb[i / 8][i % 8] = (_Float16)__builtin_amdgcn_exp2f(sc[b][i] - m[b]);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const half2v pr = {pb[t][2 * e], pb[t][2 * e + 1]};
-                l = __builtin_amdgcn_fdot2(pr, ones, l, false);
-            }
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+                for (int e = 0; e < 4; e++) {
+                    const half2v pr = {pb[t][2 * e], pb[t][2 * e + 1]};
+                    l[b] = __builtin_amdgcn_fdot2(pr, ones, l[b], false);
+                }
 #pragma unroll
-            for (int db = 0; db < 4; db++) o[db] = mfma32(va[t * 4 + db], pb[t], o[db]);
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int db = 0; db < 4; db++) o[b][db] = mfma32(va[t * 4 + db], pb[t], o[b][db]);
+        }
     }
     KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is released
-    epilogue<OutT>(p, J, row, qin, W.h, hh, m, l, o);
+#pragma unroll
+    for (int b = 0; b < QB; b++) epilogue<OutT>(p, J, row[b], qin[b], W.h, hh, m[b], l[b], o[b]);
 #if KILN_CLOCK
     if (tid == 0 && blockIdx.x < 16384) {
         g_clk[blockIdx.x][0] = __builtin_amdgcn_s_memtime() - clk0;
         g_clk[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime() - rt0;
-        for (int i = 0; i < 4; i++) g_phase[blockIdx.x][i] = ph[i];
     }
 #endif
 }
@@ -713,7 +648,5 @@ hipError_t launch_kv_prep(uint16_t* kvp, const void* k, int ldk, const void* v, 
 extern "C" int kiln_debug_clock(long long* host, int n) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kiln::g_clk), sizeof(long long) * 2 * n);
 }
-extern "C" int kiln_debug_phase(long long* host, int n) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kiln::g_phase), sizeof(long long) * 4 * n);
-}
+
 #endif

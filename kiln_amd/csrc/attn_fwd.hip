@@ -13,8 +13,10 @@
 //  * O^T = V^T P^T: P^T comes straight out of the S^T accumulator (no LDS round trip); V^T is the A
 //    operand, pre-permuted by the K/V prepare pass so that every LDS operand read of a wave is one
 //    contiguous, conflict-free 1 KB ds_read_b128.
-//  * K/V tiles (32 KB each) are double-buffered in LDS: tile j+1 is fetched from HBM/L2 into registers
-//    (coalesced 16-byte loads) while tile j is computed, then stored to the other LDS stage.
+//  * K/V stream through a ring of LDS stages filled by buffer-form global->LDS DMA, several tiles ahead.
+//  * the VALU, not the matrix core, is the tighter budget (MFMA and VALU work of a step barely overlap), so
+//    per-step vector work is cut to the softmax itself: the QK accumulator starts from -m (no subtraction
+//    before the exp), the loop is unrolled by two (no register copies of S), and DMA addressing is scalar.
 //  * Q's RMSNorm and RoPE are applied in the Q tile load, in fp32, before the single fp16 rounding.
 //  * the softmax rescale of O is lazy: the running max only moves (and O/l are only rescaled) when a
 //    tile's max exceeds it by more than 8 (log2 units), so P <= 2^8 stays far inside fp16 range.
@@ -189,17 +191,15 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 #define KILN_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (0xF << 8) | (((N) >> 4) << 14))
 
 // ------------------------------------------------------------------------------------------------
-// The kernel. A wave owns QB query blocks of 32 rows (QB = 2: 64 rows), a workgroup NW waves
-// (BM = NW * QB * 32 rows, 128 by default), two workgroups per CU. With QB = 2 each wave has two
-// independent MFMA dependency chains per phase, K/V operand reads, the DMA and the barrier are shared by
-// both blocks, and the register budget (one wave per SIMD) lets the compiler keep the O accumulators in
-// AGPRs, where the matrix cores update them without competing with the VALU for VGPR ports.
+// The kernel. A wave owns QB query blocks of 32 rows, a workgroup NW waves (BM = NW * QB * 32 = 128
+// rows), two workgroups per CU. QB = 1 (two waves per SIMD) is the default; QB = 2 (64 rows per wave, one
+// wave per SIMD, operand reads and DMA shared by both blocks) builds and is correct but measured slower.
 //
 // Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB) through an NS-stage LDS ring filled by
-// direct global->LDS DMA (global_load_lds_dwordx4: no staging registers, no ds_write), NS-2 half tiles
-// ahead of use.
+// direct global->LDS DMA (buffer_load_dwordx4 ... lds: no staging registers, no ds_write), NS-2 half
+// tiles ahead of use.
 //
-// Software pipeline, per half tile j (S_j and max(S_j) - m in registers, K_{j+1}[0,4) operands in
+// Software pipeline, per half tile j (S_j - m and max(S_j) - m in registers, K_{j+1}[0,4) operands in
 // registers, half tiles j .. j+NS-3 resident or in flight):
 //   [rare: rescale O, l, m]                                         (the only branch)
 //   K_{j+1}[4,8), V_j[t=0] reads | QK_{j+1} MFMAs interleaved with exp/cvt/row-sum of S_j |
@@ -263,14 +263,19 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     const uint32_t lds_base = (uint32_t)(size_t)(__attribute__((address_space(3))) _Float16*)lds;
 
     // half tile jh -> stage: this thread's 16-byte pieces tid + NTHR*i; the wave's 64 lanes write 1 KB
-    // of contiguous LDS at the wave-uniform base the DMA takes from M0
+    // of contiguous LDS at the wave-uniform base the DMA takes from M0.
+    // Buffer-form DMA: the lane offset tid*16 is a constant VGPR; the half tile and piece offsets go in the
+    // SGPR soffset, so a refill costs no vector instructions. The descriptor's range is the head's K/V block.
+    const __amdgpu_buffer_rsrc_t kv_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(kvh), (short)0, (int)(kv_head_stride(Tk) * 2), 0x00020000 /* raw, CDNA */);
+    const uint32_t dma_off = (uint32_t)tid * 16;
     auto dma = [&](int jh, int stage) {
-        const _Float16* src = kvh + (size_t)jh * HT_H + tid * 8;
         _Float16* dst = lds + stage * HT_H + wv * 512;
 #pragma unroll
         for (int i = 0; i < DMA_PER_HT; i++)
-            __builtin_amdgcn_global_load_lds((const void*)(src + i * NTHR * 8),
-                                             (__attribute__((address_space(3))) void*)(dst + i * NTHR * 8), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc,
+                                                     (__attribute__((address_space(3))) void*)(dst + i * NTHR * 8),
+                                                     16, dma_off, jh * (HT_H * 2) + i * (NTHR * 16), 0, 0);
     };
     // operand reads through 32-bit LDS byte addresses: base + immediate offsets fold into ds_read_b128
     auto kptr = [&](int stage) {
@@ -291,7 +296,8 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 
     floatx16 o[QB][4];
     float m[QB], l[QB], mx[QB];
-    floatx16 sc[QB];  // S_j
+    floatx16 sc[QB], sc2[QB];  // S_j - m and S_{j+1} - m; the unrolled loop alternates their roles
+    floatx16 mneg[QB];         // -m in every accumulator item: the first QK MFMA of a chain starts from it
 #pragma unroll
     for (int b = 0; b < QB; b++) {
 #pragma unroll
@@ -314,6 +320,11 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         if (Tk < 32) mask_half(0, Tk, hh, sc[b]);
         m[b] = max16(sc[b]);  // the first half tile sets the running max
         mx[b] = 0.f;          // max(S_j) - m
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            sc[b][i] -= m[b];
+            mneg[b][i] = -m[b];
+        }
     }
 #pragma unroll
     for (int s = 0; s < 4; s++) ka[s] = kptr(1 % NS)[s * 64];
@@ -321,7 +332,8 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     // of the previous iteration, and the waitcnt pass keeps the step's own new reads in flight.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 
-    auto rescale = [&](int b) {
+    // the running max moves up by d: O and l scale by 2^-d, and S_j - m (cur) shifts by -d
+    auto rescale = [&](int b, floatx16(&cur)[QB]) {
         const float d = fmaxf(mx[b], 0.f);
         const float corr = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
@@ -330,6 +342,11 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
             for (int i = 0; i < 16; i++) o[b][db][i] *= corr;
         l[b] *= corr;
         m[b] += d;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            cur[b][i] -= d;
+            mneg[b][i] = -m[b];
+        }
     };
     auto need_rescale = [&]() {
         bool need = false;
@@ -341,11 +358,11 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     int st = 0;        // stage of half tile j
     int st2 = NS - 1;  // stage that receives half tile j+NS-1
     // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
-    auto step = [&](auto maskn_tag, int j) {
+    auto step = [&](auto maskn_tag, int j, floatx16 (&cur)[QB], floatx16 (&sn)[QB]) {
         constexpr bool MASKN = decltype(maskn_tag)::value;
         if (need_rescale()) {  // lazy rescale (rare)
 #pragma unroll
-            for (int b = 0; b < QB; b++) rescale(b);
+            for (int b = 0; b < QB; b++) rescale(b, cur);
         }
         const int st1 = st == NS - 1 ? 0 : st + 1;
         half8 va[4];
@@ -360,9 +377,8 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         KILN_FENCE();
 
         // S_{j+1} on the matrix cores while the VALU turns S_j into P_j
-        floatx16 sn[QB];
 #pragma unroll
-        for (int b = 0; b < QB; b++) sn[b] = mfma32(ka[0], qreg[b][0], floatx16{});
+        for (int b = 0; b < QB; b++) sn[b] = mfma32(ka[0], qreg[b][0], mneg[b]);
         half8 pb[QB][2];
         float la[QB], lb[QB];
 #pragma unroll
@@ -372,8 +388,8 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 #pragma unroll
             for (int b = 0; b < QB; b++) {
                 if (s > 0) sn[b] = mfma32(ka[s], qreg[b][s], sn[b]);
-                const float e0 = __builtin_amdgcn_exp2f(sc[b][2 * s] - m[b]);
-                const float e1 = __builtin_amdgcn_exp2f(sc[b][2 * s + 1] - m[b]);
+                const float e0 = __builtin_amdgcn_exp2f(cur[b][2 * s]);
+                const float e1 = __builtin_amdgcn_exp2f(cur[b][2 * s + 1]);
                 pb[b][s / 4][(2 * s) % 8] = (_Float16)e0;
                 pb[b][s / 4][(2 * s + 1) % 8] = (_Float16)e1;
                 if (s & 1) {  // row sum of the fp16-rounded P values the PV MFMA consumes
@@ -419,8 +435,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 #pragma unroll
         for (int b = 0; b < QB; b++) {
             l[b] += la[b] + lb[b];
-            mx[b] = max16(sn[b]) - m[b];
-            sc[b] = sn[b];
+            mx[b] = max16(sn[b]);
         }
         st = st1;
         KILN_FENCE();
@@ -429,16 +444,27 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     using True = std::true_type;
     using False = std::false_type;
     int j = 0;
-    for (; j < nh - 2; j++) step(False{}, j);
-    if (nh >= 2) {
-        if ((Tk & 31) != 0) step(True{}, j);
-        else step(False{}, j);
+    for (; j + 1 < nh - 2; j += 2) {
+        step(False{}, j, sc, sc2);
+        step(False{}, j + 1, sc2, sc);
+    }
+    if (j < nh - 2) {
+        step(False{}, j, sc, sc2);
         j++;
+#pragma unroll
+        for (int b = 0; b < QB; b++) sc[b] = sc2[b];
+    }
+    if (nh >= 2) {
+        if ((Tk & 31) != 0) step(True{}, j, sc, sc2);
+        else step(False{}, j, sc, sc2);
+        j++;
+#pragma unroll
+        for (int b = 0; b < QB; b++) sc[b] = sc2[b];
     }
     // last half tile: no successor
     if (need_rescale()) {
 #pragma unroll
-        for (int b = 0; b < QB; b++) rescale(b);
+        for (int b = 0; b < QB; b++) rescale(b, sc);
     }
     {
         half8 va[8];
@@ -449,7 +475,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         for (int b = 0; b < QB; b++) {
             half8 pb[2];
 #pragma unroll
-            for (int i = 0; i < 16; i++) pb[i / 8][i % 8] = (_Float16)__builtin_amdgcn_exp2f(sc[b][i] - m[b]);
+            for (int i = 0; i < 16; i++) pb[i / 8][i % 8] = (_Float16)__builtin_amdgcn_exp2f(sc[b][i]);
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll

@@ -504,24 +504,48 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 // K/V prepare: fp16 conversion (+ K RMSNorm, + K RoPE) into the tiled MFMA operand order.
 // One block per (64-key tile, head). Bandwidth-bound; runs once per K/V, not once per query tile.
 // ------------------------------------------------------------------------------------------------
+struct PrepParams {
+    KVPrepJob job[MAX_JOBS];  // blockIdx.z selects the job
+    int Tk;
+    const uint16_t* kw;
+    float eps;
+    const float* rcos;
+    const float* rsin;
+};
+
 template <typename InT, bool KNORM, bool ROPE>
-__global__ __launch_bounds__(256) void k_kv_prep(uint16_t* __restrict__ kvp, const InT* __restrict__ k, int ldk,
-                                                 const InT* __restrict__ v, int ldv, int Tk,
-                                                 const uint16_t* __restrict__ kw, float eps,
-                                                 const float* __restrict__ rcos, const float* __restrict__ rsin) {
-    __shared__ _Float16 vt[KT][HD + 8];
+__global__ __launch_bounds__(256) void k_kv_prep(const PrepParams p) {
+    __shared__ __attribute__((aligned(16))) _Float16 vt[KT][HD + 8];  // V tile, rows padded to 272 bytes
     const int tid = threadIdx.x, j = blockIdx.x, h = blockIdx.y;
-    _Float16* dstK = reinterpret_cast<_Float16*>(kvp) + (size_t)h * kv_head_stride(Tk) + (size_t)j * KV_TILE_H;
+    const KVPrepJob& jb = p.job[blockIdx.z];
+    const int Tk = p.Tk;
+    const InT* __restrict__ k = reinterpret_cast<const InT*>(jb.k);
+    const InT* __restrict__ v = reinterpret_cast<const InT*>(jb.v);
+    _Float16* dstK = reinterpret_cast<_Float16*>(jb.kvp) + (size_t)h * kv_head_stride(Tk) + (size_t)j * KV_TILE_H;
 
     const int kk = tid >> 2, qd = tid & 3;  // key within the tile, quarter of the row
     const int key = j * KT + kk;
     const bool valid = key < Tk;
 
+    // V: tile -> LDS (fp16); issued first so its loads overlap the K work
+    {
+        const InT* vr = v + (size_t)(valid ? key : 0) * jb.ldv + h * HD + 32 * qd;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float x[8];
+            if (valid) load8(vr + 8 * c, x);
+            else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = 0.f;
+            }
+            *reinterpret_cast<half8*>(&vt[kk][32 * qd + 8 * c]) = to_half8(x);
+        }
+    }
     // K: chunks c in {2qd, 2qd+1, 2qd+8, 2qd+9} (8 elements each); (c, c+8) are RoPE partners
     {
         float x[4][8];
         const int cs[4] = {2 * qd, 2 * qd + 1, 2 * qd + 8, 2 * qd + 9};
-        const InT* kr = k + (size_t)(valid ? key : 0) * ldk + h * HD;
+        const InT* kr = k + (size_t)(valid ? key : 0) * jb.ldk + h * HD;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             if (valid) load8(kr + 8 * cs[c], x[c]);
@@ -538,19 +562,19 @@ __global__ __launch_bounds__(256) void k_kv_prep(uint16_t* __restrict__ kvp, con
                 for (int e = 0; e < 8; e++) ss += x[c][e] * x[c][e];
             ss += __shfl_xor(ss, 1);
             ss += __shfl_xor(ss, 2);
-            const float r = rsqrtf(ss * (1.0f / HD) + eps);
+            const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
 #pragma unroll
             for (int c = 0; c < 4; c++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) x[c][e] = x[c][e] * r * bf16_to_f32(kw[8 * cs[c] + e]);
+                for (int e = 0; e < 8; e++) x[c][e] = x[c][e] * r * bf16_to_f32(p.kw[8 * cs[c] + e]);
         }
         if constexpr (ROPE) {
             if (valid) {
 #pragma unroll
                 for (int c = 0; c < 2; c++) {
                     float cc[8], sn[8];
-                    load8(rcos + (size_t)key * 64 + 8 * cs[c], cc);
-                    load8(rsin + (size_t)key * 64 + 8 * cs[c], sn);
+                    load8(p.rcos + (size_t)key * 64 + 8 * cs[c], cc);
+                    load8(p.rsin + (size_t)key * 64 + 8 * cs[c], sn);
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
                         const float a = x[c][e], b = x[c + 2][e];
@@ -567,32 +591,25 @@ __global__ __launch_bounds__(256) void k_kv_prep(uint16_t* __restrict__ kvp, con
             *reinterpret_cast<half8*>(dstK + kv_k_off(kb, s, kl + 32 * hb)) = to_half8(x[c]);
         }
     }
-    // V: tile -> LDS (fp16), then gather the permuted-transposed operand order
-    {
-        const InT* vr = v + (size_t)(valid ? key : 0) * ldv + h * HD + 32 * qd;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float x[8];
-            if (valid) load8(vr + 8 * c, x);
-            else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) x[e] = 0.f;
-            }
-            *reinterpret_cast<half8*>(&vt[kk][32 * qd + 8 * c]) = to_half8(x);
-        }
-    }
     __syncthreads();
+    // V^T operand units (c, t, db, lane): 8 keys of one d. ds_read_b64_tr_b16 (gfx950) transposes within
+    // each group of 16 lanes: source lane r supplies 4 halves of row r/4, and lane i receives element e of
+    // row 4e + i/4, column i%4. Lane r pointing at vt[key0 + r/4][d0 + 4(r%4)] therefore leaves lane i
+    // holding vt[key0 + e][d0 + i], e = 0..3: four consecutive keys of its own d, one read per 4 keys.
     {
-        // unit (c, t, db, lane): 8 keys of one d; thread -> (c, t) = (tid >> 7, (tid >> 6) & 1), 4 db each
         const int c = tid >> 7, t = (tid >> 6) & 1, ln = tid & 63;
-        const int kbase = 32 * c + 16 * t + 4 * (ln >> 5);
+        const int g = ln >> 4, i = ln & 15;
+        const int key0 = 32 * c + 16 * t + 4 * (g >> 1);
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s4 lds_s4;
 #pragma unroll
         for (int db = 0; db < 4; db++) {
-            const int d = db * 32 + (ln & 31);
-            half8 o;
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++) o[jj] = vt[kbase + 8 * (jj >> 2) + (jj & 3)][d];
-            *reinterpret_cast<half8*>(dstK + kv_v_off(c, t, db, ln)) = o;
+            const int d0 = 32 * db + 16 * (g & 1);
+            const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[key0 + (i >> 2)][d0 + 4 * (i & 3)]);
+            const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[key0 + 8 + (i >> 2)][d0 + 4 * (i & 3)]);
+            typedef short s8 __attribute__((ext_vector_type(8)));
+            const s8 o = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            *reinterpret_cast<s8*>(dstK + kv_v_off(c, t, db, ln)) = o;
         }
     }
 }
@@ -649,23 +666,28 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
 }
 
 template <typename InT>
-static hipError_t dispatch_prep(uint16_t* kvp, const void* k, int ldk, const void* v, int ldv, int Tk, int H,
-                                const uint16_t* kw, float eps, const float* rc, const float* rs, hipStream_t s) {
-    dim3 grid(kv_tiles(Tk), H), block(256);
-    const InT* kk = reinterpret_cast<const InT*>(k);
-    const InT* vv = reinterpret_cast<const InT*>(v);
-    if (kw && rc) hipLaunchKernelGGL((k_kv_prep<InT, true, true>), grid, block, 0, s, kvp, kk, ldk, vv, ldv, Tk, kw, eps, rc, rs);
-    else if (kw) hipLaunchKernelGGL((k_kv_prep<InT, true, false>), grid, block, 0, s, kvp, kk, ldk, vv, ldv, Tk, kw, eps, rc, rs);
-    else if (rc) hipLaunchKernelGGL((k_kv_prep<InT, false, true>), grid, block, 0, s, kvp, kk, ldk, vv, ldv, Tk, kw, eps, rc, rs);
-    else hipLaunchKernelGGL((k_kv_prep<InT, false, false>), grid, block, 0, s, kvp, kk, ldk, vv, ldv, Tk, kw, eps, rc, rs);
+static hipError_t dispatch_prep(const PrepParams& p, int njobs, int H, hipStream_t s) {
+    dim3 grid(kv_tiles(p.Tk), H, njobs), block(256);
+    if (p.kw && p.rcos) hipLaunchKernelGGL((k_kv_prep<InT, true, true>), grid, block, 0, s, p);
+    else if (p.kw) hipLaunchKernelGGL((k_kv_prep<InT, true, false>), grid, block, 0, s, p);
+    else if (p.rcos) hipLaunchKernelGGL((k_kv_prep<InT, false, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((k_kv_prep<InT, false, false>), grid, block, 0, s, p);
     return hipGetLastError();
 }
 
-hipError_t launch_kv_prep(uint16_t* kvp, const void* k, int ldk, const void* v, int ldv, DT in, int Tk, int H,
-                          const uint16_t* kw, float eps, const float* rcos, const float* rsin, hipStream_t s) {
-    if (Tk <= 0 || H <= 0) return hipSuccess;
-    if (in == DT::F16) return dispatch_prep<_Float16>(kvp, k, ldk, v, ldv, Tk, H, kw, eps, rcos, rsin, s);
-    return dispatch_prep<float>(kvp, k, ldk, v, ldv, Tk, H, kw, eps, rcos, rsin, s);
+hipError_t launch_kv_prep(const KVPrepJob* jobs, int njobs, DT in, int Tk, int H, const uint16_t* kw, float eps,
+                          const float* rcos, const float* rsin, hipStream_t s) {
+    if (Tk <= 0 || H <= 0 || njobs <= 0) return hipSuccess;
+    if (njobs > MAX_JOBS) return hipErrorInvalidValue;
+    PrepParams p{};
+    for (int i = 0; i < njobs; i++) p.job[i] = jobs[i];
+    p.Tk = Tk;
+    p.kw = kw;
+    p.eps = eps;
+    p.rcos = rcos;
+    p.rsin = rsin;
+    if (in == DT::F16) return dispatch_prep<_Float16>(p, njobs, H, s);
+    return dispatch_prep<float>(p, njobs, H, s);
 }
 
 }  // namespace kiln

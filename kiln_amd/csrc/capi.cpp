@@ -106,14 +106,14 @@ int flash_self(void* out, DT od, int ldo, long long bso, const void* q, int ldq,
     }
     const size_t isz = in == DT::F16 ? 2 : 4, osz = od == DT::F16 ? 2 : 4;
     kiln::AttnLaunch a{};
+    kiln::KVPrepJob pj[kiln::MAX_JOBS];
     for (int b = 0; b < B; b++) {
         uint16_t* kvp = reinterpret_cast<uint16_t*>((char*)ws + per * b);
-        int r = hip_check(kiln::launch_kv_prep(kvp, (const char*)k + bsk * b * isz, ldk, (const char*)v + bsv * b * isz,
-                                               ldv, in, Tk, H, kw, eps, rc, rs, stream),
-                          "kv_prep launch");
-        if (r) return r;
+        pj[b] = {kvp, (const char*)k + bsk * b * isz, (const char*)v + bsv * b * isz, ldk, ldv};
         a.job[b] = {(const char*)q + bsq * b * isz, kvp, (char*)out + bso * b * osz, Tk, npad};
     }
+    int r = hip_check(kiln::launch_kv_prep(pj, B, in, Tk, H, kw, eps, rc, rs, stream), "kv_prep launch");
+    if (r) return r;
     a.njobs = B;
     a.Tq = Tq;
     a.H = H;
@@ -170,8 +170,8 @@ int kiln_kv_prepare(uint16_t* kvp, const void* k, int ldk, const void* v, int ld
     if (!rows_ok(k, ldk, in) || !rows_ok(v, ldv, in)) return fail(KILN_EUNSUPPORTED, "K/V rows not 16-byte aligned");
     if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(KILN_EINVAL, "rope tables: need both cos and sin");
     if (rope_cos && (!aligned16(rope_cos) || !aligned16(rope_sin))) return fail(KILN_EUNSUPPORTED, "rope tables not 16-byte aligned");
-    return hip_check(kiln::launch_kv_prep(kvp, k, ldk, v, ldv, in, Tk, H, k_norm_w, eps, rope_cos, rope_sin,
-                                          (hipStream_t)stream),
+    const kiln::KVPrepJob pj{kvp, k, v, ldk, ldv};
+    return hip_check(kiln::launch_kv_prep(&pj, 1, in, Tk, H, k_norm_w, eps, rope_cos, rope_sin, (hipStream_t)stream),
                      "kv_prep launch");
 }
 

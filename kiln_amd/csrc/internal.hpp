@@ -31,8 +31,17 @@ struct AttnLaunch {
 
 hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s);
 
-hipError_t launch_kv_prep(uint16_t* kvp, const void* k, int ldk, const void* v, int ldv, DT in, int Tk, int H,
-                          const uint16_t* kw, float eps, const float* rcos, const float* rsin, hipStream_t s);
+// One K/V context to prepare: raw K and V rows (row strides ldk, ldv; head h at column h*128) into the
+// tiled fp16 buffer kvp.
+struct KVPrepJob {
+    uint16_t* kvp;
+    const void* k;
+    const void* v;
+    int ldk, ldv;
+};
+// Prepares njobs (<= MAX_JOBS) contexts of Tk keys and H heads in one launch (K RMSNorm with kw, RoPE).
+hipError_t launch_kv_prep(const KVPrepJob* jobs, int njobs, DT in, int Tk, int H, const uint16_t* kw, float eps,
+                          const float* rcos, const float* rsin, hipStream_t s);
 
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s);

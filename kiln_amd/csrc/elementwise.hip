@@ -2,6 +2,8 @@
 // and the exact fp32 attention used when the fp16 path does not apply (causal, Dh != 128, fp32 mode).
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -105,9 +107,70 @@ __global__ __launch_bounds__(256) void k_nag(T* a, int lda, const T* an, int ldn
     }
 }
 
+// Row-per-wave NAG for rows of up to 64 x 8 x NAG_CH elements in 16-byte-aligned chunks of 8: every lane
+// loads its chunks once (vector loads), the two L1 sums are wave reductions, and the blend is computed from
+// the registers (one read pass instead of two).
+constexpr int NAG_CH = 4;
+template <typename T>
+__global__ __launch_bounds__(256) void k_nag_rows(T* a, int lda, const T* an, int ldn, int T_, int dim, float s,
+                                                  float tau, float alpha) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= T_) return;
+    T* p = a + (size_t)row * lda;
+    const T* n = an + (size_t)row * ldn;
+    float pv[NAG_CH][8], g[NAG_CH][8];
+    float lp = 0.f, lg = 0.f;
+#pragma unroll
+    for (int c = 0; c < NAG_CH; c++) {
+        const int i = (c * 64 + lane) * 8;
+        if (i < dim) {
+            float nv[8];
+            load8(p + i, pv[c]);
+            load8(n + i, nv);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                g[c][e] = pv[c][e] * s - nv[e] * (s - 1.f);
+                lp += fabsf(pv[c][e]);
+                lg += fabsf(g[c][e]);
+            }
+        }
+    }
+    lp = wave_sum(lp);
+    lg = wave_sum(lg);
+    const float ratio = lg / fmaxf(lp, 1e-12f);
+    const float k = ratio > tau ? tau / ratio : 1.f;
+#pragma unroll
+    for (int c = 0; c < NAG_CH; c++) {
+        const int i = (c * 64 + lane) * 8;
+        if (i < dim) {
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = alpha * g[c][e] * k + (1.f - alpha) * pv[c][e];
+            if constexpr (std::is_same<T, float>::value) {
+                *reinterpret_cast<floatx4*>(p + i) = floatx4{o[0], o[1], o[2], o[3]};
+                *reinterpret_cast<floatx4*>(p + i + 4) = floatx4{o[4], o[5], o[6], o[7]};
+            } else {
+                *reinterpret_cast<half8*>(p + i) = to_half8(o);
+            }
+        }
+    }
+}
+
 hipError_t launch_nag(void* a, int lda, const void* an, int ldn, DT dt, int T, int dim, float sc, float tau,
                       float alpha, hipStream_t s) {
     if (T <= 0) return hipSuccess;
+    const size_t esz = dt == DT::F16 ? 2 : 4;
+    const bool vec = dim % 8 == 0 && dim <= 64 * 8 * NAG_CH && ((uintptr_t)a % 16) == 0 && ((uintptr_t)an % 16) == 0 &&
+                     ((size_t)lda * esz) % 16 == 0 && ((size_t)ldn * esz) % 16 == 0;
+    if (vec) {
+        if (dt == DT::F16)
+            hipLaunchKernelGGL(k_nag_rows<_Float16>, dim3((T + 3) / 4), dim3(256), 0, s, (_Float16*)a, lda,
+                               (const _Float16*)an, ldn, T, dim, sc, tau, alpha);
+        else
+            hipLaunchKernelGGL(k_nag_rows<float>, dim3((T + 3) / 4), dim3(256), 0, s, (float*)a, lda, (const float*)an,
+                               ldn, T, dim, sc, tau, alpha);
+        return hipGetLastError();
+    }
     if (dt == DT::F16)
         hipLaunchKernelGGL(k_nag<_Float16>, dim3(T), dim3(256), 0, s, (_Float16*)a, lda, (const _Float16*)an, ldn, dim,
                            sc, tau, alpha);

@@ -288,3 +288,20 @@ def test_rmsnorm_rope_nag_kernels(gpu):
         torch.cuda.synchronize()
         r = oracle.nag(a.to(dt).float().numpy(), an.to(dt).float().numpy())
         assert_close(ad.float().cpu().numpy(), r, f"nag {dt}", max_abs=tol, mean_abs=tol / 10)
+
+
+@pytest.mark.parametrize("dim", [2048, 520, 1000, 2056])
+def test_nag_combine_widths(gpu, dim):
+    """Row-per-wave vector path (dim % 8 == 0, dim <= 2048) and the general path (other widths) of the NAG
+    blend (engine/src/dit.cu:295-324), fp16 and fp32, against the oracle on rows where the clamp engages
+    (tau < ratio) and rows where it does not."""
+    T = 37
+    a = randn(65, T, dim) * 0.1
+    an = randn(66, T, dim) * 0.1
+    an[: T // 2] = a[: T // 2] * 0.9  # ratio < tau: no clamp
+    for dt, tol in ((torch.float32, 1e-5), (torch.float16, 2e-3)):
+        ad = a.to(dt).to(DEV)
+        kiln_amd.nag_combine(ad, an.to(dt).to(DEV))
+        torch.cuda.synchronize()
+        r = oracle.nag(a.to(dt).float().numpy(), an.to(dt).float().numpy())
+        assert_close(ad.float().cpu().numpy(), r, f"nag dim={dim} {dt}", max_abs=tol, mean_abs=tol / 10)

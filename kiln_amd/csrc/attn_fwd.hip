@@ -247,16 +247,6 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     if (!decode_work(p, W)) return;
     const AttnJob J = p.job[W.jb];
 
-    int row[QB];
-    bool qin[QB];
-    half8 qreg[QB][8];
-#pragma unroll
-    for (int b = 0; b < QB; b++) {
-        row[b] = W.qt * BM + (wv * QB + b) * 32 + (lane & 31);
-        qin[b] = row[b] < p.Tq;
-        load_q<InT, QNORM, ROPE>(p, J.q, row[b], qin[b], W.h, hh, qreg[b]);
-    }
-
     const int Tk = J.Tk;
     const int nh = (Tk + 31) / 32;  // half tiles holding real keys
     const _Float16* kvh = reinterpret_cast<const _Float16*>(J.kv) + (size_t)W.h * kv_head_stride(Tk);
@@ -288,9 +278,19 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         return pair_max(fmaxf(fmaxf(fmaxf(x0, x1), x2), fmaxf(fmaxf(x3, x4), a[15])));
     };
 
-    // prologue: half tiles 0 .. NS-2 in flight; wait for tiles 0 and 1
+    // prologue: half tiles 0 .. NS-2 in flight, then the Q tile loads (their latencies overlap); wait for
+    // tiles 0 and 1
 #pragma unroll
     for (int i = 0; i < NS - 1; i++) dma(min(i, nh - 1), i);
+    int row[QB];
+    bool qin[QB];
+    half8 qreg[QB][8];
+#pragma unroll
+    for (int b = 0; b < QB; b++) {
+        row[b] = W.qt * BM + (wv * QB + b) * 32 + (lane & 31);
+        qin[b] = row[b] < p.Tq;
+        load_q<InT, QNORM, ROPE>(p, J.q, row[b], qin[b], W.h, hh, qreg[b]);
+    }
     KILN_WAIT_VMCNT((NS - 3) * DMA_PER_HT);
     __builtin_amdgcn_s_barrier();
 

@@ -305,3 +305,16 @@ def test_nag_combine_widths(gpu, dim):
         torch.cuda.synchronize()
         r = oracle.nag(a.to(dt).float().numpy(), an.to(dt).float().numpy())
         assert_close(ad.float().cpu().numpy(), r, f"nag dim={dim} {dt}", max_abs=tol, mean_abs=tol / 10)
+
+
+def test_prepare_multi_tile_blocks_ragged(gpu):
+    """Long context (Tk = 5000: 79 tiles per head, the last holding 8 keys): the K/V prepare pass walks
+    several tiles per block there, so a block's last tile is ragged and the tile-ahead loads run past Tk.
+    fp32 inputs through attention16 (engine/src/gpu.h:155-156)."""
+    Tq, Tk = 64, 5000
+    q, k, v = _qkv(81, Tq, Tk, scale_qk=1.0)
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), H)
+    out = torch.empty(Tq, H * D, dtype=torch.float16, device=DEV)
+    kiln_amd.attention16(out, q.to(DEV), k.to(DEV), v.to(DEV), Tq, Tk, H, D)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), ref, f"attention16 Tq={Tq} Tk={Tk}")

@@ -318,3 +318,48 @@ def test_prepare_multi_tile_blocks_ragged(gpu):
     kiln_amd.attention16(out, q.to(DEV), k.to(DEV), v.to(DEV), Tq, Tk, H, D)
     torch.cuda.synchronize()
     assert_close(out.float().cpu().numpy(), ref, f"attention16 Tq={Tq} Tk={Tk}")
+
+
+def test_prepped_entry_points(gpu):
+    """kiln_kv_prepare (K RMSNorm + RoPE) then kiln_attn_fwd_prepped / kiln_attn_fwd_prepped_batch (Q RMSNorm +
+    RoPE in the Q load): the split form of the fused DiT call, single and batched, fp32 and fp16 outputs,
+    with npad zero keys; and kiln_attn_fwd_exact called directly."""
+    Hp, Wp, npad = 12, 20, 7
+    T = Hp * Wp
+    g = torch.Generator().manual_seed(91)
+    qw = (torch.rand(D, generator=g) * 0.5 + 0.75).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=g) * 0.5 + 0.75).to(torch.bfloat16)
+    cos, sin = oracle.cosmos_rope(Hp, Wp)
+    rope = (torch.from_numpy(cos).to(DEV), torch.from_numpy(sin).to(DEV))
+    qwb = qw.view(torch.int16).numpy().view(np.uint16)
+    kwb = kw.view(torch.int16).numpy().view(np.uint16)
+    Bn = 3
+    qs = [torch.randn(T, H * D, generator=g).half() for _ in range(Bn)]
+    ks = [torch.randn(T, H * D, generator=g).half() for _ in range(Bn)]
+    vs = [torch.randn(T, H * D, generator=g).half() for _ in range(Bn)]
+    refs = []
+    for b in range(Bn):
+        qn = oracle.rope_half(oracle.rmsnorm_rows(qs[b].float().numpy(), qwb).reshape(T, H * D), H, cos, sin)
+        kn = oracle.rope_half(oracle.rmsnorm_rows(ks[b].float().numpy(), kwb).reshape(T, H * D), H, cos, sin)
+        refs.append(oracle.attn_f64(qn, kn, vs[b].float().numpy(), H, npad=npad))
+    kvps = [kiln_amd.kv_prepare(ks[b].to(DEV), vs[b].to(DEV), H, k_norm_w=kw.to(DEV), rope=rope) for b in range(Bn)]
+
+    out = torch.empty(T, H * D, dtype=torch.float32, device=DEV)
+    kiln_amd.attn_prepped(out, qs[1].to(DEV), kvps[1], T, H, npad=npad, q_norm_w=qw.to(DEV), rope=rope)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), refs[1], "attn_fwd_prepped fp32 out")
+
+    outb = torch.empty(Bn * T, H * D, dtype=torch.float16, device=DEV)
+    kiln_amd.attn_prepped_batch(outb, torch.cat(qs).to(DEV), kvps, T, T, H, npad=npad, q_norm_w=qw.to(DEV),
+                                rope=rope)
+    torch.cuda.synchronize()
+    o = outb.float().cpu().numpy()
+    for b in range(Bn):
+        assert_close(o[b * T:(b + 1) * T], refs[b], f"attn_fwd_prepped_batch item {b}")
+
+    q, k, v = _qkv(92, 50, 70, scale_qk=1.0)
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), H, npad=3)
+    oe = torch.empty(50, H * D, device=DEV)
+    kiln_amd.attention_exact(oe, q.to(DEV), k.to(DEV), v.to(DEV), 50, 70, H, D, npad=3)
+    torch.cuda.synchronize()
+    assert_close(oe.cpu().numpy(), ref, "attn_fwd_exact Dh=128", max_abs=1e-5, mean_abs=1e-6)

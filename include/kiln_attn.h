@@ -13,6 +13,8 @@
  * row stride ld in elements; head h occupies columns [h*Dh, (h+1)*Dh). Rows must be 16-byte
  * aligned. Keys beyond Tk are never read; npad extra all-zero keys (K = 0, V = 0) are accounted for
  * analytically (they add npad*exp(-max) to the softmax denominator and nothing to the output).
+ * The Dh = 128 flash path takes up to 2^22 keys per head (KILN_EUNSUPPORTED above; the reference's
+ * longest context is 6144).
  *
  * fp16 values cross the ABI as uint16_t bit patterns (IEEE binary16), bf16 norm weights likewise.
  */

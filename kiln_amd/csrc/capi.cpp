@@ -79,8 +79,13 @@ bool rows_ok(const void* p, int ld, DT dt) {
     return dt == DT::F16 ? (ld % 8) == 0 : (ld % 4) == 0;
 }
 
+// Keys per head of the flash path: the attention kernel addresses a head's prepared K/V block (32 KB per 64
+// keys) with 32-bit buffer offsets.
+constexpr int MAX_TK = 1 << 22;
+
 int check_common(int Tq, int Tk, int H, int npad) {
     if (Tq < 0 || Tk < 0 || H <= 0 || npad < 0) return fail(KILN_EINVAL, "bad sizes Tq=%d Tk=%d H=%d npad=%d", Tq, Tk, H, npad);
+    if (Tk > MAX_TK) return fail(KILN_EUNSUPPORTED, "Tk=%d above %d keys per head", Tk, MAX_TK);
     if (Tk == 0 && npad == 0 && Tq > 0) return fail(KILN_EINVAL, "no keys (Tk=0, npad=0): softmax undefined");
     return KILN_OK;
 }
@@ -164,6 +169,7 @@ int kiln_kv_prepare(uint16_t* kvp, const void* k, int ldk, const void* v, int ld
     if (in_dtype != KILN_F32 && in_dtype != KILN_F16) return fail(KILN_EINVAL, "in_dtype %d", in_dtype);
     DT in = (DT)in_dtype;
     if (Tk < 0 || H <= 0) return fail(KILN_EINVAL, "bad sizes Tk=%d H=%d", Tk, H);
+    if (Tk > MAX_TK) return fail(KILN_EUNSUPPORTED, "Tk=%d above %d keys per head", Tk, MAX_TK);
     if (Tk == 0) return KILN_OK;
     if (!kvp || !k || !v) return fail(KILN_EINVAL, "null pointer");
     if (!aligned16(kvp)) return fail(KILN_EUNSUPPORTED, "kvp not 16-byte aligned");
@@ -348,13 +354,14 @@ int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const 
     kiln::AttnLaunch a{};
     int n = 0;
     for (int b = 0; b < B; b++) {
-        if (Lk[b] <= 0 || npad[b] < 0 || !kvp[b] || !aligned16(kvp[b]))
+        if (Lk[b] <= 0 || Lk[b] > MAX_TK || npad[b] < 0 || !kvp[b] || !aligned16(kvp[b]))
             return fail(KILN_EINVAL, "context %d: Lk=%d npad=%d", b, Lk[b], npad[b]);
         a.job[n++] = {(const char*)q + (size_t)b * T * ldq * isz, kvp[b], (char*)out + (size_t)b * T * ldo * osz, Lk[b],
                       npad[b]};
     }
     if (kvp_neg) {
-        if (Lk_neg <= 0 || npad_neg < 0 || !aligned16(kvp_neg)) return fail(KILN_EINVAL, "NAG context Lk=%d", Lk_neg);
+        if (Lk_neg <= 0 || Lk_neg > MAX_TK || npad_neg < 0 || !aligned16(kvp_neg))
+            return fail(KILN_EINVAL, "NAG context Lk=%d", Lk_neg);
         a.job[n++] = {q, kvp_neg, out_neg, Lk_neg, npad_neg};
     }
     a.njobs = n;

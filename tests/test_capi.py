@@ -63,6 +63,11 @@ def test_argument_validation_without_gpu(L):
     assert L.kiln_attn_fwd_f32out(p, 2048, p, 2048, p, 2048, p, 2048, 8, 0, 16, 128, 0, 0, None) == kiln_amd.KILN_EINVAL
     # negative sizes
     assert L.kiln_attn_fwd_f32out(p, 2048, p, 2048, p, 2048, p, 2048, -1, 8, 16, 128, 0, 0, None) == kiln_amd.KILN_EINVAL
+    # flash path: 32-bit buffer offsets bound the keys per head
+    assert L.kiln_attn_fwd_f32out(p, 2048, p, 2048, p, 2048, p, 2048, 8, (1 << 22) + 1, 16, 128, 0, 0, None) == \
+        kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_kv_prepare(p, p, 2048, p, 2048, 1, (1 << 22) + 1, 16, None, 1e-6, None, None, None) == \
+        kiln_amd.KILN_EUNSUPPORTED
     # exact path: head size bound
     assert L.kiln_attn_fwd_exact(p, 4096, p, 4096, p, 4096, p, 4096, 8, 8, 8, 512, 0, 0, None) == kiln_amd.KILN_EUNSUPPORTED
     # dtype codes

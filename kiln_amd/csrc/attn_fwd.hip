@@ -506,7 +506,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 // ------------------------------------------------------------------------------------------------
 struct PrepParams {
     KVPrepJob job[MAX_JOBS];  // blockIdx.z selects the job
-    int Tk, tpb;              // keys; 64-key tiles per block
+    int Tk, tpb;              // keys; 32-key half tiles per block
     const uint16_t* kw;
     float eps;
     const float* rcos;
@@ -534,144 +534,139 @@ struct Chunk8<float> {
     __device__ __forceinline__ float operator[](int e) const { return e < 4 ? a[e] : b[e - 4]; }
 };
 
-// All global loads of one 64-key tile for one thread: K chunks {2qd, 2qd+1, 2qd+8, 2qd+9} of key kk (the
-// (c, c+8) pairs are RoPE partners), V chunks 4qd..4qd+3 of key kk, and the key's RoPE cos/sin for the first
-// two K chunks. Loaded a tile ahead of use, so a block's reads of tile j+1 overlap its stores of tile j.
+// All global loads of one 32-key half tile for one thread (8 threads per key): K chunks q8 and q8+8 of key
+// kk (RoPE partners: d and d+64), V chunks 2q8 and 2q8+1, and the key's RoPE cos/sin for K chunk q8.
+// Loaded a half tile ahead of use, so a block's reads of the next half tile overlap its stores.
 template <typename InT, bool ROPE>
-struct PrepTile {
-    Chunk8<InT> k[4], v[4];
-    floatx4 rc[2][2], rs[2][2];
+struct PrepHalf {
+    Chunk8<InT> k[2], v[2];
+    floatx4 rc[2], rs[2];
 };
 
 template <typename InT, bool KNORM, bool ROPE>
 __global__ __launch_bounds__(256) void k_kv_prep(const PrepParams p) {
-    __shared__ __attribute__((aligned(16))) _Float16 vt[KT][HD + 8];  // V tile, rows padded to 272 bytes
+    // V half tile in fp16, rows padded to 288 bytes: the transposing reads of one 16-lane group touch 4 rows
+    // 8 banks apart, conflict-free
+    __shared__ __attribute__((aligned(16))) _Float16 vt[32][HD + 16];
     const int tid = threadIdx.x, h = blockIdx.y;
     const KVPrepJob& jb = p.job[blockIdx.z];
-    const int Tk = p.Tk, ntiles = kv_tiles(Tk);
-    const int t0 = blockIdx.x * p.tpb, t1 = min(t0 + p.tpb, ntiles);
+    const int Tk = p.Tk, nhalf = 2 * kv_tiles(Tk);
+    const int t0 = blockIdx.x * p.tpb, t1 = min(t0 + p.tpb, nhalf);
     if (t0 >= t1) return;
     const InT* __restrict__ k = reinterpret_cast<const InT*>(jb.k);
     const InT* __restrict__ v = reinterpret_cast<const InT*>(jb.v);
     _Float16* dst_h = reinterpret_cast<_Float16*>(jb.kvp) + (size_t)h * kv_head_stride(Tk);
-    const int kk = tid >> 2, qd = tid & 3;  // key within the tile, quarter of the row
-    const int cs[4] = {2 * qd, 2 * qd + 1, 2 * qd + 8, 2 * qd + 9};
-    float kwf[4][8];
+    const int kk = tid >> 3, q8 = tid & 7;  // key within the half tile, eighth of the row
+    float kwf[2][8];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
+    for (int c = 0; c < 2; c++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) kwf[c][e] = KNORM ? bf16_to_f32(p.kw[8 * cs[c] + e]) : 1.f;
+        for (int e = 0; e < 8; e++) kwf[c][e] = KNORM ? bf16_to_f32(p.kw[8 * (q8 + 8 * c) + e]) : 1.f;
 
-    auto load_tile = [&](int j, PrepTile<InT, ROPE>& t) {
-        const int key = j * KT + kk;
+    auto load_half = [&](int jh, PrepHalf<InT, ROPE>& t) {
+        const int key = jh * 32 + kk;
         if (key < Tk) {
-            const InT* kr = k + (size_t)key * jb.ldk + h * HD;
-            const InT* vr = v + (size_t)key * jb.ldv + h * HD + 32 * qd;
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                t.k[c].load(kr + 8 * cs[c]);
-                t.v[c].load(vr + 8 * c);
-            }
+            const InT* kr = k + (size_t)key * jb.ldk + h * HD + 8 * q8;
+            const InT* vr = v + (size_t)key * jb.ldv + h * HD + 16 * q8;
+            t.k[0].load(kr);
+            t.k[1].load(kr + 64);
+            t.v[0].load(vr);
+            t.v[1].load(vr + 8);
             if constexpr (ROPE) {
-#pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    const float* cp = p.rcos + (size_t)key * 64 + 8 * cs[c];
-                    const float* sp = p.rsin + (size_t)key * 64 + 8 * cs[c];
-                    t.rc[c][0] = *reinterpret_cast<const floatx4*>(cp);
-                    t.rc[c][1] = *reinterpret_cast<const floatx4*>(cp + 4);
-                    t.rs[c][0] = *reinterpret_cast<const floatx4*>(sp);
-                    t.rs[c][1] = *reinterpret_cast<const floatx4*>(sp + 4);
-                }
+                const float* cp = p.rcos + (size_t)key * 64 + 8 * q8;
+                const float* sp = p.rsin + (size_t)key * 64 + 8 * q8;
+                t.rc[0] = *reinterpret_cast<const floatx4*>(cp);
+                t.rc[1] = *reinterpret_cast<const floatx4*>(cp + 4);
+                t.rs[0] = *reinterpret_cast<const floatx4*>(sp);
+                t.rs[1] = *reinterpret_cast<const floatx4*>(sp + 4);
             }
         } else {  // keys past Tk: zeros (the attention kernel relies on a zero-padded last tile)
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
+            for (int c = 0; c < 2; c++) {
                 t.k[c].zero();
                 t.v[c].zero();
             }
-            if constexpr (ROPE) {
-#pragma unroll
-                for (int c = 0; c < 2; c++) t.rc[c][0] = t.rc[c][1] = t.rs[c][0] = t.rs[c][1] = floatx4{};
-            }
+            if constexpr (ROPE) t.rc[0] = t.rc[1] = t.rs[0] = t.rs[1] = floatx4{};
         }
     };
 
-    PrepTile<InT, ROPE> cur, nxt;
-    load_tile(t0, cur);
-    for (int j = t0; j < t1; j++) {
-        if (j + 1 < t1) load_tile(j + 1, nxt);
-        _Float16* dstK = dst_h + (size_t)j * KV_TILE_H;
-        // V: tile -> LDS (fp16)
+    PrepHalf<InT, ROPE> cur, nxt;
+    load_half(t0, cur);
+    for (int jh = t0; jh < t1; jh++) {
+        if (jh + 1 < t1) load_half(jh + 1, nxt);
+        // half tile jh of the prepared buffer: [K_c 8 KB | V_c 8 KB] (K_c and V_c orders in common.hpp)
+        _Float16* dst = dst_h + (size_t)(jh >> 1) * KV_TILE_H;
+        const int c = jh & 1;
+        // V: half tile -> LDS (fp16)
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int cc = 0; cc < 2; cc++) {
             half8 hv;
 #pragma unroll
-            for (int e = 0; e < 8; e++) hv[e] = (_Float16)cur.v[c][e];
-            *reinterpret_cast<half8*>(&vt[kk][32 * qd + 8 * c]) = hv;
+            for (int e = 0; e < 8; e++) hv[e] = (_Float16)cur.v[cc][e];
+            *reinterpret_cast<half8*>(&vt[kk][16 * q8 + 8 * cc]) = hv;
         }
-        // K: RMSNorm (4 threads per key), RoPE, fp16, into the K_c operand order
+        // K: RMSNorm (8 threads per key), RoPE, fp16, into the K_c operand order
         {
-            float x[4][8];
+            float x[2][8];
 #pragma unroll
-            for (int c = 0; c < 4; c++)
+            for (int cc = 0; cc < 2; cc++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) x[c][e] = cur.k[c][e];
+                for (int e = 0; e < 8; e++) x[cc][e] = cur.k[cc][e];
             if constexpr (KNORM) {
                 float ss = 0.f;
 #pragma unroll
-                for (int c = 0; c < 4; c++)
+                for (int cc = 0; cc < 2; cc++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++) ss += x[c][e] * x[c][e];
+                    for (int e = 0; e < 8; e++) ss += x[cc][e] * x[cc][e];
                 ss += __shfl_xor(ss, 1);
                 ss += __shfl_xor(ss, 2);
+                ss += __shfl_xor(ss, 4);
                 const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
 #pragma unroll
-                for (int c = 0; c < 4; c++)
+                for (int cc = 0; cc < 2; cc++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++) x[c][e] = x[c][e] * r * kwf[c][e];
+                    for (int e = 0; e < 8; e++) x[cc][e] = x[cc][e] * r * kwf[cc][e];
             }
             if constexpr (ROPE) {
 #pragma unroll
-                for (int c = 0; c < 2; c++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        const float cc = cur.rc[c][e / 4][e % 4], sn = cur.rs[c][e / 4][e % 4];
-                        const float a = x[c][e], b = x[c + 2][e];
-                        x[c][e] = a * cc - b * sn;
-                        x[c + 2][e] = b * cc + a * sn;
-                    }
+                for (int e = 0; e < 8; e++) {
+                    const float cs = cur.rc[e / 4][e % 4], sn = cur.rs[e / 4][e % 4];
+                    const float a = x[0][e], b = x[1][e];
+                    x[0][e] = a * cs - b * sn;
+                    x[1][e] = b * cs + a * sn;
+                }
             }
-            const int kb = kk >> 5, kl = kk & 31;
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int s = cs[c] >> 1, hb = cs[c] & 1;
-                *reinterpret_cast<half8*>(dstK + kv_k_off(kb, s, kl + 32 * hb)) = to_half8(x[c]);
+            for (int cc = 0; cc < 2; cc++) {
+                const int ch = q8 + 8 * cc;  // 8-element chunk of the row: d = 8 ch
+                *reinterpret_cast<half8*>(dst + kv_k_off(c, ch >> 1, kk + 32 * (ch & 1))) = to_half8(x[cc]);
             }
         }
         __syncthreads();
-        // V^T operand units (c, t, db, lane): 8 keys of one d. ds_read_b64_tr_b16 (gfx950) transposes within
-        // each group of 16 lanes: source lane r supplies 4 halves of row r/4, and lane i receives element e
-        // of row 4e + i/4, column i%4. Lane r pointing at vt[key0 + r/4][d0 + 4(r%4)] therefore leaves lane
-        // i holding vt[key0 + e][d0 + i], e = 0..3: four consecutive keys of its own d.
+        // V^T operand units (t, db, lane): 8 keys of one d. ds_read_b64_tr_b16 (gfx950) transposes within each
+        // group of 16 lanes: source lane r supplies 4 halves of row r/4, and lane i receives element e of row
+        // 4e + i/4, column i%4. Lane r pointing at vt[key0 + r/4][d0 + 4(r%4)] therefore leaves lane i holding
+        // vt[key0 + e][d0 + i], e = 0..3: four consecutive keys of its own d.
         {
-            const int c = tid >> 7, t = (tid >> 6) & 1, ln = tid & 63;
+            const int w = tid >> 6, ln = tid & 63, t = w >> 1;
             const int g = ln >> 4, i = ln & 15;
-            const int key0 = 32 * c + 16 * t + 4 * (g >> 1);
+            const int key0 = 16 * t + 4 * (g >> 1);
             typedef short s4 __attribute__((ext_vector_type(4)));
             typedef short s8 __attribute__((ext_vector_type(8)));
             typedef __attribute__((address_space(3))) s4 lds_s4;
 #pragma unroll
-            for (int db = 0; db < 4; db++) {
+            for (int dd = 0; dd < 2; dd++) {
+                const int db = 2 * (w & 1) + dd;
                 const int d0 = 32 * db + 16 * (g & 1);
                 const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[key0 + (i >> 2)][d0 + 4 * (i & 3)]);
                 const s4 hi =
                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[key0 + 8 + (i >> 2)][d0 + 4 * (i & 3)]);
                 const s8 o = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                *reinterpret_cast<s8*>(dstK + kv_v_off(c, t, db, ln)) = o;
+                *reinterpret_cast<s8*>(dst + kv_v_off(c, t, db, ln)) = o;
             }
         }
-        if (j + 1 < t1) {
-            __syncthreads();  // vt is rewritten by the next tile
+        if (jh + 1 < t1) {
+            __syncthreads();  // vt is rewritten by the next half tile
             cur = nxt;
         }
     }
@@ -728,14 +723,9 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
     return dispatch_attn<float, float>(p, units, qn, rp, s);
 }
 
-#ifndef KILN_PREP_BLOCKS
-#define KILN_PREP_BLOCKS 1024
-#endif
-constexpr int PREP_BLOCKS = KILN_PREP_BLOCKS;
-
 template <typename InT>
 static hipError_t dispatch_prep(const PrepParams& p, int njobs, int H, hipStream_t s) {
-    dim3 grid((kv_tiles(p.Tk) + p.tpb - 1) / p.tpb, H, njobs), block(256);
+    dim3 grid((2 * kv_tiles(p.Tk) + p.tpb - 1) / p.tpb, H, njobs), block(256);
     if (p.kw && p.rcos) hipLaunchKernelGGL((k_kv_prep<InT, true, true>), grid, block, 0, s, p);
     else if (p.kw) hipLaunchKernelGGL((k_kv_prep<InT, true, false>), grid, block, 0, s, p);
     else if (p.rcos) hipLaunchKernelGGL((k_kv_prep<InT, false, true>), grid, block, 0, s, p);
@@ -750,10 +740,10 @@ hipError_t launch_kv_prep(const KVPrepJob* jobs, int njobs, DT in, int Tk, int H
     PrepParams p{};
     for (int i = 0; i < njobs; i++) p.job[i] = jobs[i];
     p.Tk = Tk;
-    // about PREP_BLOCKS blocks, each walking tpb consecutive tiles of one head with the next tile's loads in
-    // flight (one block per tile would put every block of the grid in the same load-then-store phase)
-    const int tiles = kv_tiles(Tk) * H * njobs;
-    p.tpb = min(max((tiles + PREP_BLOCKS - 1) / PREP_BLOCKS, 1), 16);
+    // each block walks two consecutive 32-key half tiles of one head, the second one's loads in flight while
+    // the first is converted and stored (measured best at T = 1536 and 4096; one per block for small inputs)
+    const int halves = 2 * kv_tiles(Tk) * H * njobs;
+    p.tpb = halves >= 1024 ? 2 : 1;
     p.kw = kw;
     p.eps = eps;
     p.rcos = rcos;

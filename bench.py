@@ -25,6 +25,7 @@ sys.path.insert(0, ROOT)
 METRIC = "attention TFLOP/s + % fp16 MFMA peak at S=1536/4096; ms attn per DiT step"
 PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 flop/clk
 H, D = 16, 128
+WARM_S = 0.2  # seconds of untimed sustained work before each timed loop
 
 
 def log(*a):
@@ -51,9 +52,17 @@ class Timer:
 
     def run(self, fn, steps, warmup):
         torch = self.torch
+        # untimed warm-up: `warmup` calls, then more until ~WARM_S of GPU work has run, so the timed loop
+        # sees the clock the GPU settles at under sustained matrix-core load (it ramps and overshoots
+        # for several ms after an idle period)
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < WARM_S:
+            for _ in range(max(1, warmup)):
+                fn()
+            torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()

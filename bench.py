@@ -132,6 +132,20 @@ def dit_step_case(torch, kiln_amd, dev, nblocks=28, Hp=48, Wp=72, B=2, L=512, se
     return dict(T=T, step=step, flop=flop)
 
 
+def run_probe():
+    """Runs kiln_amd/probe/mfma_mix (built by kiln_amd/build.py) in a child process; {} if it is not built."""
+    import subprocess
+    exe = os.path.join(ROOT, "kiln_amd", "probe", "mfma_mix")
+    if not os.path.exists(exe):
+        log("bench.py: kiln_amd/probe/mfma_mix is not built; no sustained-throughput probe")
+        return {}
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        log(f"bench.py: probe failed ({r.returncode}): {r.stderr.strip()}")
+        return {}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def cpu_baseline(case, target_s=10.0):
     """The reference's fp32 two-pass attention (bench/flash_test.cu:10-32, restated in oracle/oracle.c) with
     the QK-RMSNorm and RoPE passes (kernels.cu:656-666, 759-772) on config 4: whole CFG items while they fit
@@ -176,6 +190,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--main-only", action="store_true",
                     help="run only the config-4 attention kernel loop (for rocprofv3 runs)")
+    ap.add_argument("--probe", action="store_true",
+                    help="only run the sustained matrix-core probe (kiln_amd/probe/mfma_mix) and print its JSON")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
                     help="copy a MIB-sized device buffer --steps times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -183,6 +199,10 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path has no "
               f"collective and shards by head with no communication, so run with --gpus 1.", file=sys.stderr)
         return 2
+
+    if args.probe:
+        print(json.dumps(run_probe()), flush=True)
+        return 0
 
     import torch
     import kiln_amd
@@ -234,6 +254,9 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("traffic_bytes")
 
+    probe = run_probe()
+    log(f"sustained matrix-core probe: {probe}")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg4)
@@ -271,6 +294,13 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(tf4_main / PEAK_TFLOPS, 4),
             "traffic": traffic,
+            # what the chip sustains under a long matrix-core load (kiln_amd/probe/mfma_mix): pure
+            # v_mfma_f32_32x32x16_f16 on random fp16 data, and the same with the key loop's per-MFMA side
+            # work (1 KB LDS operand read, one exp2, two FMAs); the spec peak assumes 2.4 GHz
+            "sustained_mfma_tflops": probe.get("mfma32_tflops"),
+            "sustained_mix_tflops": probe.get("mix32_tflops"),
+            "frac_of_sustained_mfma": (round(tf4_main / probe["mfma32_tflops"], 4)
+                                       if probe.get("mfma32_tflops") else None),
         },
         "cpu_baseline": cpu,
     }

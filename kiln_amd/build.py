@@ -48,6 +48,13 @@ def build(verbose=False):
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)
+    # sustained matrix-core probe (a measurement aid for bench.py --probe, not part of the library)
+    probe = os.path.join(HERE, "probe", "mfma_mix")
+    cmd = [HIPCC, *FLAGS, "-Wno-unused-result", os.path.join(HERE, "probe", "mfma_mix.hip"), "-o", probe + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"probe build failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(probe + ".tmp", probe)
     return LIB
 
 

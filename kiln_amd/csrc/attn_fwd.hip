@@ -88,21 +88,66 @@ __device__ __forceinline__ bool decode_work(const AttnParams& p, Work& w) {
     return true;
 }
 
+// 8 consecutive input elements as loaded (16 B of fp16 or 32 B of fp32)
+template <typename InT>
+struct Chunk8;
+template <>
+struct Chunk8<_Float16> {
+    half8 v;
+    __device__ __forceinline__ void load(const _Float16* p) { v = *reinterpret_cast<const half8*>(p); }
+    __device__ __forceinline__ void zero() { v = half8{}; }
+    __device__ __forceinline__ float operator[](int e) const { return (float)v[e]; }
+};
+template <>
+struct Chunk8<float> {
+    floatx4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = *reinterpret_cast<const floatx4*>(p);
+        b = *reinterpret_cast<const floatx4*>(p + 4);
+    }
+    __device__ __forceinline__ void zero() { a = b = floatx4{}; }
+    __device__ __forceinline__ float operator[](int e) const { return e < 4 ? a[e] : b[e - 4]; }
+};
+
 // Q tile of one lane: query `row`, d chunks {16s + 8hh .. +8} for s = 0..7 (the B operands of S^T = K Q^T),
 // RMSNorm and RoPE applied in fp32, pre-scaled by log2(e)/sqrt(128), rounded once to fp16.
 template <typename InT, bool QNORM, bool ROPE>
 __device__ __forceinline__ void load_q(const AttnParams& p, const void* q, int row, bool qin, int h, int hh,
                                        half8 (&qreg)[8]) {
-    float x[8][8];
-    const InT* qr = reinterpret_cast<const InT*>(q) + (size_t)(qin ? row : 0) * p.ldq + h * HD + 8 * hh;
+    // Every load (Q row, RoPE rows, norm weights) is issued before any of them is used, unconditionally (rows
+    // past Tq read row 0 and are zeroed afterwards): one memory round trip for the whole tile. A per-lane
+    // branch around a load, or a conversion scheduled between loads, serializes them.
+    const int rr = qin ? row : 0;
+    const InT* qr = reinterpret_cast<const InT*>(q) + (size_t)rr * p.ldq + h * HD + 8 * hh;
+    Chunk8<InT> raw[8];
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-        if (qin) load8(qr + 16 * s, x[s]);
-        else {
+    for (int s = 0; s < 8; s++) raw[s].load(qr + 16 * s);
+    floatx4 cr[4][2], sr[4][2];
+    if constexpr (ROPE) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[s][e] = 0.f;
+        for (int s = 0; s < 4; s++) {
+            const float* cp = p.rcos + (size_t)rr * 64 + 16 * s + 8 * hh;
+            const float* sp = p.rsin + (size_t)rr * 64 + 16 * s + 8 * hh;
+            cr[s][0] = *reinterpret_cast<const floatx4*>(cp);
+            cr[s][1] = *reinterpret_cast<const floatx4*>(cp + 4);
+            sr[s][0] = *reinterpret_cast<const floatx4*>(sp);
+            sr[s][1] = *reinterpret_cast<const floatx4*>(sp + 4);
         }
     }
+    uint16_t wb[8][8];
+    if constexpr (QNORM) {
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) wb[s][e] = p.qw[16 * s + 8 * hh + e];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    float x[8][8];
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[s][e] = qin ? raw[s][e] : 0.f;
     if constexpr (QNORM) {
         float ss = 0.f;
 #pragma unroll
@@ -112,27 +157,20 @@ __device__ __forceinline__ void load_q(const AttnParams& p, const void* q, int r
         ss = pair_sum(ss);
         const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const uint16_t* wp = p.qw + 16 * s + 8 * hh;
+        for (int s = 0; s < 8; s++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[s][e] = x[s][e] * r * bf16_to_f32(wp[e]);
-        }
+            for (int e = 0; e < 8; e++) x[s][e] = x[s][e] * r * bf16_to_f32(wb[s][e]);
     }
     if constexpr (ROPE) {
-        if (qin) {
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                float c[8], sn[8];
-                load8(p.rcos + (size_t)row * 64 + 16 * s + 8 * hh, c);
-                load8(p.rsin + (size_t)row * 64 + 16 * s + 8 * hh, sn);
+        for (int s = 0; s < 4; s++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float a = x[s][e], b = x[s + 4][e];
-                    x[s][e] = a * c[e] - b * sn[e];
-                    x[s + 4][e] = b * c[e] + a * sn[e];
-                }
+            for (int e = 0; e < 8; e++) {
+                const float cs = cr[s][e / 4][e % 4], sn = sr[s][e / 4][e % 4];
+                const float a = x[s][e], b = x[s + 4][e];
+                x[s][e] = a * cs - b * sn;
+                x[s + 4][e] = b * cs + a * sn;
             }
-        }
     }
 #pragma unroll
     for (int s = 0; s < 8; s++) {
@@ -282,6 +320,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     // tiles 0 and 1
 #pragma unroll
     for (int i = 0; i < NS - 1; i++) dma(min(i, nh - 1), i);
+    __builtin_amdgcn_sched_barrier(0);
     int row[QB];
     bool qin[QB];
     half8 qreg[QB][8];
@@ -511,27 +550,6 @@ struct PrepParams {
     float eps;
     const float* rcos;
     const float* rsin;
-};
-
-// 8 consecutive input elements as loaded (16 B of fp16 or 32 B of fp32)
-template <typename InT>
-struct Chunk8;
-template <>
-struct Chunk8<_Float16> {
-    half8 v;
-    __device__ __forceinline__ void load(const _Float16* p) { v = *reinterpret_cast<const half8*>(p); }
-    __device__ __forceinline__ void zero() { v = half8{}; }
-    __device__ __forceinline__ float operator[](int e) const { return (float)v[e]; }
-};
-template <>
-struct Chunk8<float> {
-    floatx4 a, b;
-    __device__ __forceinline__ void load(const float* p) {
-        a = *reinterpret_cast<const floatx4*>(p);
-        b = *reinterpret_cast<const floatx4*>(p + 4);
-    }
-    __device__ __forceinline__ void zero() { a = b = floatx4{}; }
-    __device__ __forceinline__ float operator[](int e) const { return e < 4 ? a[e] : b[e - 4]; }
 };
 
 // All global loads of one 32-key half tile for one thread (8 threads per key): K chunks q8 and q8+8 of key

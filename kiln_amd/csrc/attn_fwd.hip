@@ -188,20 +188,6 @@ __device__ __forceinline__ void mask_half(int jh, int Tk, int hh, floatx16& a) {
         if (kbase + 8 * (i / 4) + (i % 4) >= Tk) a[i] = -INFINITY;
 }
 
-// lazy rescale: only when the running max grows by more than RESCALE_TH (wave-uniform branch)
-__device__ __forceinline__ void maybe_rescale(float mx, float& m, float& l, floatx16 (&o)[4]) {
-    const float mnew = fmaxf(m, mx);
-    if (__builtin_amdgcn_ballot_w64(mnew > m + RESCALE_TH)) {
-        const float corr = __builtin_amdgcn_exp2f(m - mnew);
-#pragma unroll
-        for (int db = 0; db < 4; db++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[db][i] *= corr;
-        l *= corr;
-        m = mnew;
-    }
-}
-
 // full row sum (lane pair), npad zero keys (tcflash.cuh:136-147), normalize, store this lane's row
 template <typename OutT>
 __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, int row, bool qin, int h, int hh,

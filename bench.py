@@ -248,6 +248,21 @@ def main():
         f"{cfg5['flop'] / ms5 / 1e9:.1f} TFLOP/s")
     del cfg5
 
+    # the DiT block's HBM-bound passes around attention at config 5's CFG batch (2 x 3456 rows x 2048):
+    # modulated LayerNorm to fp16 (read 4 B, write 2 B per element) and the gated residual (read 8, write 4)
+    R5 = 2 * 3456
+    x5 = torch.randn(R5, H * D, device=dev)
+    y5 = torch.randn(R5, H * D, device=dev)
+    sc5, sh5 = torch.randn(H * D, device=dev) * 0.1, torch.randn(H * D, device=dev)
+    n16 = torch.empty(R5, H * D, dtype=torch.float16, device=dev)
+    ms_ln = tm.run(lambda: kiln_amd.layernorm_mod(n16, x5, sc5, sh5), args.steps * 5, args.warmup)
+    ms_ag = tm.run(lambda: kiln_amd.add_gated(x5, y5, sc5), args.steps * 5, args.warmup)
+    ln_tbps = 6.0 * R5 * H * D / ms_ln / 1e9
+    ag_tbps = 12.0 * R5 * H * D / ms_ag / 1e9
+    log(f"layernorm_mod16 (6912 x 2048): {ms_ln * 1e3:.1f} us {ln_tbps:.2f} TB/s; add_gated: {ms_ag * 1e3:.1f} us "
+        f"{ag_tbps:.2f} TB/s")
+    del x5, y5, n16
+
     traffic = None  # HBM bytes per launch of k_attn_fwd (config 4), from the committed rocprofv3 FETCH/WRITE runs
     tpath = os.path.join(ROOT, "profiles", "k_attn_fwd_config4_hbm_traffic.json")
     if os.path.exists(tpath):
@@ -285,6 +300,10 @@ def main():
             "s1536_ms_per_call": round(ms2, 5),
             "dit_step_attention_ms": round(ms5, 4),
             "dit_step_workload": "config 5: 768x1152 (T=3456), B=2, 28 blocks x (self + cross L=512 + NAG)",
+            "layernorm_mod16_us": round(ms_ln * 1e3, 2),
+            "layernorm_mod16_tbps": round(ln_tbps, 3),
+            "add_gated_us": round(ms_ag * 1e3, 2),
+            "add_gated_tbps": round(ag_tbps, 3),
         },
         "roofline": {
             "bound": "mfma",

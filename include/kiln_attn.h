@@ -82,6 +82,21 @@ int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const flo
 int kiln_nag_combine(void* a, int lda, const void* an, int ldn, int dtype, int T, int dim, float s, float tau,
                      float alpha, kiln_stream_t stream);
 
+/* Replaces layernorm_mod() (engine/src/gpu.h:134, impl engine/src/kernels.cu:678-692): the DiT block's
+ * modulated LayerNorm, per row of `dim`: y = (x - mean) * rsqrt(var + eps) * (1 + scale) + shift, with
+ * scale/shift per column (fp32 [dim]). x, y [rows, dim] dense fp32. */
+int kiln_layernorm_mod(float* y, const float* x, const float* scale, const float* shift, int rows, int dim, float eps,
+                       kiln_stream_t stream);
+
+/* Replaces layernorm_mod16() (engine/src/gpu.h:135, impl engine/src/kernels.cu:693-697): the same with an fp16
+ * output (the input of the fp16-activation projections, engine/src/dit.cu:460,474,491). */
+int kiln_layernorm_mod16(uint16_t* y, const float* x, const float* scale, const float* shift, int rows, int dim,
+                         float eps, kiln_stream_t stream);
+
+/* Replaces add_gated() (engine/src/gpu.h:136, impl engine/src/kernels.cu:700-708): the gated residual
+ * x += gate * y per row (gate fp32 [dim], NULL = 1). x, y [rows, dim] dense fp32. */
+int kiln_add_gated(float* x, const float* y, const float* gate, int rows, int dim, kiln_stream_t stream);
+
 /* Host-side Cosmos 3D RoPE tables for an Hp x Wp patch grid (engine/src/dit.cu:196-215):
  * cos_t, sin_t are HOST arrays of Hp*Wp*64 floats. */
 int kiln_cosmos_rope_tables(float* cos_t, float* sin_t, int Hp, int Wp);

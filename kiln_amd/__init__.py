@@ -32,6 +32,9 @@ _SIGS = {
     "kiln_attn_fwd_exact": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "kiln_rmsnorm_rows": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     "kiln_rope_half": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "kiln_layernorm_mod": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
+    "kiln_layernorm_mod16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
+    "kiln_add_gated": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "kiln_nag_combine": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _f, _f, _f, _vp]),
     "kiln_cosmos_rope_tables": (_i, [_vp, _vp, _i, _i]),
     "kiln_kv_prepped_bytes": (_sz, [_i, _i]),
@@ -156,6 +159,22 @@ def rmsnorm(y, x, w=None, rows=None, dim=128, eps=1e-6, stream=None):
 def rope_half(x, T, H, Dh, cos_t, sin_t, stream=None):
     """rope_half() (engine/src/gpu.h:145): in place on dense fp32 rows [T, H*Dh]."""
     _check(lib().kiln_rope_half(_ptr(x), T, H, Dh, _ptr(cos_t), _ptr(sin_t), _stream(stream)))
+    return x
+
+
+def layernorm_mod(y, x, scale, shift, eps=1e-6, stream=None):
+    """Modulated LayerNorm of the DiT block (engine/src/kernels.cu:678-697): x [rows, dim] fp32, y fp32 or fp16."""
+    import torch
+    rows, dim = x.shape
+    fn = lib().kiln_layernorm_mod16 if y.dtype == torch.float16 else lib().kiln_layernorm_mod
+    _check(fn(_ptr(y), _ptr(x), _ptr(scale), _ptr(shift), rows, dim, eps, _stream(stream)))
+    return y
+
+
+def add_gated(x, y, gate=None, stream=None):
+    """Gated residual x += gate * y (engine/src/kernels.cu:700-708); x, y [rows, dim] fp32."""
+    rows, dim = x.shape
+    _check(lib().kiln_add_gated(_ptr(x), _ptr(y), _ptr(gate), rows, dim, _stream(stream)))
     return x
 
 

@@ -387,6 +387,28 @@ int kiln_rmsnorm_rows(float* y, const float* x, const uint16_t* w_bf16, int rows
     return hip_check(kiln::launch_rmsnorm_rows(y, x, w_bf16, rows, dim, eps, (hipStream_t)stream), "rmsnorm launch");
 }
 
+int kiln_layernorm_mod(float* y, const float* x, const float* scale, const float* shift, int rows, int dim, float eps,
+                       kiln_stream_t stream) {
+    if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes rows=%d dim=%d", rows, dim);
+    if (rows && (!y || !x || !scale || !shift)) return fail(KILN_EINVAL, "null pointer");
+    return hip_check(kiln::launch_layernorm_mod(y, kiln::DT::F32, x, scale, shift, rows, dim, eps, (hipStream_t)stream),
+                     "layernorm_mod launch");
+}
+
+int kiln_layernorm_mod16(uint16_t* y, const float* x, const float* scale, const float* shift, int rows, int dim,
+                         float eps, kiln_stream_t stream) {
+    if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes rows=%d dim=%d", rows, dim);
+    if (rows && (!y || !x || !scale || !shift)) return fail(KILN_EINVAL, "null pointer");
+    return hip_check(kiln::launch_layernorm_mod(y, kiln::DT::F16, x, scale, shift, rows, dim, eps, (hipStream_t)stream),
+                     "layernorm_mod16 launch");
+}
+
+int kiln_add_gated(float* x, const float* y, const float* gate, int rows, int dim, kiln_stream_t stream) {
+    if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes rows=%d dim=%d", rows, dim);
+    if (rows && (!x || !y)) return fail(KILN_EINVAL, "null pointer");
+    return hip_check(kiln::launch_add_gated(x, y, gate, rows, dim, (hipStream_t)stream), "add_gated launch");
+}
+
 int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {
     if (T < 0 || H <= 0 || Dh <= 0 || Dh % 2) return fail(KILN_EINVAL, "bad sizes");
     if (T && (!x || !cos_t || !sin_t)) return fail(KILN_EINVAL, "null pointer");

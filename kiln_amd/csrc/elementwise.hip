@@ -54,6 +54,135 @@ hipError_t launch_rmsnorm_rows(float* y, const float* x, const uint16_t* w, int 
     return hipGetLastError();
 }
 
+__device__ __forceinline__ float ldv(const float* p) { return *p; }
+__device__ __forceinline__ float ldv(const _Float16* p) { return (float)*p; }
+__device__ __forceinline__ void stv(float* p, float v) { *p = v; }
+__device__ __forceinline__ void stv(_Float16* p, float v) { *p = (_Float16)v; }
+
+// ---- modulated LayerNorm of the DiT block (engine/src/kernels.cu:678-697): one wave per row ----
+// y = (x - mean) * rsqrt(var + eps) * (1 + scale) + shift, mean and var over the row (two passes, as the
+// reference). Rows of up to 64 lanes x NC float4 chunks stay in registers: one HBM read, one write.
+__device__ __forceinline__ void st4(float* p, floatx4 v) { *reinterpret_cast<floatx4*>(p) = v; }
+__device__ __forceinline__ void st4(_Float16* p, floatx4 v) {
+    half4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    *reinterpret_cast<half4*>(p) = h;
+}
+
+template <typename OutT, int NC>
+__global__ __launch_bounds__(256) void k_layernorm_mod_rows(OutT* y, const float* x, const float* scale,
+                                                            const float* shift, int rows, int dim, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * dim;
+    OutT* yr = y + (size_t)row * dim;
+    const int nc = dim / 4;
+    floatx4 v[NC], sc[NC], sh[NC];  // the row and its modulation, all loads issued before the reductions
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        const int c = min(lane + 64 * k, nc - 1);
+        v[k] = *reinterpret_cast<const floatx4*>(xr + 4 * c);
+        sc[k] = *reinterpret_cast<const floatx4*>(scale + 4 * c);
+        sh[k] = *reinterpret_cast<const floatx4*>(shift + 4 * c);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < NC; k++)
+        if (lane + 64 * k < nc) s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+    const float mean = wave_sum(s) / (float)dim;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < NC; k++)
+        if (lane + 64 * k < nc)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float d = v[k][e] - mean;
+                q += d * d;
+            }
+    const float r = rsqrtf(wave_sum(q) / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        const int c = lane + 64 * k;
+        if (c < nc) {
+            floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = (v[k][e] - mean) * r * (1.f + sc[k][e]) + sh[k][e];
+            st4(yr + 4 * c, o);
+        }
+    }
+}
+
+// any dim / alignment: three passes over the row (the second and third hit the cache)
+template <typename OutT>
+__global__ __launch_bounds__(256) void k_layernorm_mod_any(OutT* y, const float* x, const float* scale,
+                                                           const float* shift, int rows, int dim, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * dim;
+    OutT* yr = y + (size_t)row * dim;
+    float s = 0.f;
+    for (int i = lane; i < dim; i += 64) s += xr[i];
+    const float mean = wave_sum(s) / (float)dim;
+    float q = 0.f;
+    for (int i = lane; i < dim; i += 64) {
+        const float d = xr[i] - mean;
+        q += d * d;
+    }
+    const float r = rsqrtf(wave_sum(q) / (float)dim + eps);
+    for (int i = lane; i < dim; i += 64) stv(yr + i, (xr[i] - mean) * r * (1.f + scale[i]) + shift[i]);
+}
+
+template <typename OutT>
+static hipError_t layernorm_mod_sel(OutT* y, const float* x, const float* scale, const float* shift, int rows, int dim,
+                                    float eps, bool vec, hipStream_t s) {
+    const dim3 grid((rows + 3) / 4), block(256);
+    const int nc = dim / 4;
+    if (vec && nc <= 64 * 2) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 2>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    else if (vec && nc <= 64 * 4) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 4>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    else if (vec && nc <= 64 * 8) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 8>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    else if (vec && nc <= 64 * 16) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 16>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    else hipLaunchKernelGGL((k_layernorm_mod_any<OutT>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_layernorm_mod(void* y, DT out, const float* x, const float* scale, const float* shift, int rows,
+                                int dim, float eps, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    const size_t osz = out == DT::F16 ? 2 : 4;
+    auto al = [](const void* p, size_t a) { return ((uintptr_t)p % a) == 0; };
+    const bool vec = dim % 4 == 0 && al(x, 16) && al(scale, 16) && al(shift, 16) && al(y, 4 * osz);
+    if (out == DT::F16) return layernorm_mod_sel((_Float16*)y, x, scale, shift, rows, dim, eps, vec, s);
+    return layernorm_mod_sel((float*)y, x, scale, shift, rows, dim, eps, vec, s);
+}
+
+// ---- gated residual (engine/src/kernels.cu:700-708): x += (gate ? gate[col] : 1) * y ----
+__global__ __launch_bounds__(256) void k_add_gated4(float* x, const float* y, const float* gate, size_t n4, int dim4) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    floatx4 a = reinterpret_cast<floatx4*>(x)[i];
+    const floatx4 b = reinterpret_cast<const floatx4*>(y)[i];
+    const floatx4 g = gate ? reinterpret_cast<const floatx4*>(gate)[i % dim4] : floatx4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int e = 0; e < 4; e++) a[e] += g[e] * b[e];
+    reinterpret_cast<floatx4*>(x)[i] = a;
+}
+__global__ __launch_bounds__(256) void k_add_gated1(float* x, const float* y, const float* gate, size_t n, int dim) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] += (gate ? gate[i % dim] : 1.f) * y[i];
+}
+
+hipError_t launch_add_gated(float* x, const float* y, const float* gate, int rows, int dim, hipStream_t s) {
+    const size_t n = (size_t)rows * dim;
+    if (n == 0) return hipSuccess;
+    auto al = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+    if (dim % 4 == 0 && al(x) && al(y) && (!gate || al(gate))) {
+        const size_t n4 = n / 4;
+        hipLaunchKernelGGL(k_add_gated4, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x, y, gate, n4, dim / 4);
+    } else {
+        hipLaunchKernelGGL(k_add_gated1, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, gate, n, dim);
+    }
+    return hipGetLastError();
+}
+
 // ---- rotate-half RoPE (engine/src/kernels.cu:759-772): one thread per rotated pair ----
 __global__ __launch_bounds__(256) void k_rope_half(float* x, int T, int H, int Dh, const float* ct, const float* st) {
     const int half = Dh / 2;
@@ -78,10 +207,6 @@ hipError_t launch_rope_half(float* x, int T, int H, int Dh, const float* c, cons
 }
 
 // ---- NAG combine (engine/src/dit.cu:295-324): one block per token row, fp32 arithmetic ----
-__device__ __forceinline__ float ldv(const float* p) { return *p; }
-__device__ __forceinline__ float ldv(const _Float16* p) { return (float)*p; }
-__device__ __forceinline__ void stv(float* p, float v) { *p = v; }
-__device__ __forceinline__ void stv(_Float16* p, float v) { *p = (_Float16)v; }
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_nag(T* a, int lda, const T* an, int ldn, int dim, float s, float tau,

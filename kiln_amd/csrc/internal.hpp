@@ -48,6 +48,9 @@ hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const
 
 hipError_t launch_rmsnorm_rows(float* y, const float* x, const uint16_t* w, int rows, int dim, float eps, hipStream_t s);
 hipError_t launch_rope_half(float* x, int T, int H, int Dh, const float* c, const float* sn, hipStream_t s);
+hipError_t launch_layernorm_mod(void* y, DT out, const float* x, const float* scale, const float* shift, int rows,
+                                int dim, float eps, hipStream_t s);
+hipError_t launch_add_gated(float* x, const float* y, const float* gate, int rows, int dim, hipStream_t s);
 hipError_t launch_nag(void* a, int lda, const void* an, int ldn, DT dt, int T, int dim, float sc, float tau,
                       float alpha, hipStream_t s);
 

@@ -61,6 +61,21 @@ inline void rope_half(float* x, int T, int H, int Dh, const float* cos_t, const 
     check(kiln_rope_half(x, T, H, Dh, cos_t, sin_t, (kiln_stream_t)stream_ref()), "rope_half");
 }
 
+// Modulated LayerNorm of the DiT block, fp32 or fp16 output (scale/shift fp32 per column).
+inline void layernorm_mod(float* y, const float* x, const float* scale, const float* shift, int rows, int dim,
+                          float eps) {
+    check(kiln_layernorm_mod(y, x, scale, shift, rows, dim, eps, (kiln_stream_t)stream_ref()), "layernorm_mod");
+}
+inline void layernorm_mod16(uint16_t* y, const float* x, const float* scale, const float* shift, int rows, int dim,
+                            float eps) {
+    check(kiln_layernorm_mod16(y, x, scale, shift, rows, dim, eps, (kiln_stream_t)stream_ref()), "layernorm_mod16");
+}
+
+// Gated residual x += gate * y (gate may be null).
+inline void add_gated(float* x, const float* y, const float* gate, int rows, int dim) {
+    check(kiln_add_gated(x, y, gate, rows, dim, (kiln_stream_t)stream_ref()), "add_gated");
+}
+
 // NAG combine of fp16 rows (the k_nag<__half> launch of the fp16-activation forward).
 inline void nag16(uint16_t* a, const uint16_t* an, int T, int dim, float scale, float tau, float alpha) {
     check(kiln_nag_combine(a, dim, an, dim, KILN_F16, T, dim, scale, tau, alpha, (kiln_stream_t)stream_ref()),

@@ -30,6 +30,8 @@ def lib():
                                       ctypes.c_double]
         L.oracle_attn_f16sem.argtypes = [_f32p, _i, _f32p, _i, _f32p, _i, _f32p, _i, _i, _i, _i, _i, _i]
         L.oracle_rmsnorm_rows.argtypes = [_f32p, _f32p, ctypes.c_void_p, ctypes.c_long, _i, ctypes.c_float]
+        L.oracle_layernorm_mod.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_long, _i, ctypes.c_float]
+        L.oracle_add_gated.argtypes = [_f32p, _f32p, ctypes.c_void_p, ctypes.c_long, _i]
         L.oracle_rope_half.argtypes = [_f32p, _i, _i, _i, _i, _f32p, _f32p]
         L.oracle_cosmos_rope.argtypes = [_f32p, _f32p, _i, _i]
         L.oracle_nag.argtypes = [_f32p, _i, _f32p, _i, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float]
@@ -74,6 +76,23 @@ def attn_f16sem(q, k, v, H, npad=0, out16=True):
     out = np.empty((q.shape[0], H * 128), np.float32)
     lib().oracle_attn_f16sem(out, out.shape[1], q, q.shape[1], k, k.shape[1], v, v.shape[1], q.shape[0], k.shape[0],
                              H, npad, int(out16))
+    return out
+
+
+def layernorm_mod(x, scale, shift, eps=1e-6):
+    """Modulated LayerNorm over the rows of x [rows, dim] (engine/src/kernels.cu:678-697); new array."""
+    x = _c32(x)
+    y = np.empty_like(x)
+    lib().oracle_layernorm_mod(y, x, _c32(scale), _c32(shift), x.shape[0], x.shape[1], eps)
+    return y
+
+
+def add_gated(x, y, gate=None):
+    """x + gate * y per row (engine/src/kernels.cu:700-708); new array."""
+    out = _c32(x).copy()
+    y = _c32(y)
+    g = _c32(gate) if gate is not None else None
+    lib().oracle_add_gated(out, y, g.ctypes.data if g is not None else None, out.shape[0], out.shape[1])
     return out
 
 

@@ -260,6 +260,43 @@ void oracle_rmsnorm_rows(float* y, const float* x, const uint16_t* w_bf16, long 
 }
 
 /*
+ * Modulated LayerNorm of the DiT block (engine/src/kernels.cu:678-697, k_layernorm_mod; called as
+ * layernorm_mod / layernorm_mod16 at engine/src/dit.cu:460,474,491), per row of `dim`:
+ *   mean = sum(x)/dim;  var = sum((x - mean)^2)/dim;  y = (x - mean) * rsqrt(var + eps) * (1 + scale) + shift
+ * scale/shift are per column. fp32 arithmetic in the reference's order (two passes).
+ * Pinned: equals torch layer_norm (no affine) * (1 + scale) + shift in float64; scale = shift = 0 gives
+ * rows of mean 0 and variance 1.
+ */
+void oracle_layernorm_mod(float* y, const float* x, const float* scale, const float* shift, long rows, int dim,
+                          float eps) {
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * dim;
+        float* yr = y + (size_t)r * dim;
+        float s = 0.f;
+        for (int i = 0; i < dim; i++) s += xr[i];
+        const float mean = s / (float)dim;
+        float v = 0.f;
+        for (int i = 0; i < dim; i++) {
+            const float d = xr[i] - mean;
+            v += d * d;
+        }
+        const float rr = 1.0f / sqrtf(v / (float)dim + eps);
+        for (int i = 0; i < dim; i++) yr[i] = (xr[i] - mean) * rr * (1.f + scale[i]) + shift[i];
+    }
+}
+
+/*
+ * Gated residual (engine/src/kernels.cu:700-708, k_add_gated): x[r][i] += (gate ? gate[i] : 1) * y[r][i].
+ * Pinned: gate = NULL is plain addition; gate = 0 leaves x unchanged.
+ */
+void oracle_add_gated(float* x, const float* y, const float* gate, long rows, int dim) {
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; r++)
+        for (int i = 0; i < dim; i++) x[(size_t)r * dim + i] += (gate ? gate[i] : 1.f) * y[(size_t)r * dim + i];
+}
+
+/*
  * Rotate-half RoPE (engine/src/kernels.cu:759-772, k_rope_half), in place on x [T, H*Dh]
  * (row stride ld elements), tables [T, Dh/2]:
  *   a = p[i], b = p[i+half];  p[i] = a*c - b*s;  p[i+half] = b*c + a*s

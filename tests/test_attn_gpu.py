@@ -363,3 +363,51 @@ def test_prepped_entry_points(gpu):
     kiln_amd.attention_exact(oe, q.to(DEV), k.to(DEV), v.to(DEV), 50, 70, H, D, npad=3)
     torch.cuda.synchronize()
     assert_close(oe.cpu().numpy(), ref, "attn_fwd_exact Dh=128", max_abs=1e-5, mean_abs=1e-6)
+
+
+# ---- modulated LayerNorm and gated residual of the DiT block ----
+@pytest.mark.parametrize("rows,dim,offset", [(6912, 2048, 0), (37, 2048, 1), (64, 1000, 0), (9, 6144, 0)])
+def test_layernorm_mod(gpu, rows, dim, offset):
+    """kiln_layernorm_mod / _mod16 against the oracle: fp32 out to fp32 rounding (the row sums add in another
+    order), fp16 out within one fp16 ulp plus that fp32 difference (values near zero have tiny ulps).
+    (6912, 2048) is config 5's CFG batch (2 x 3456 tokens); offset 1 makes the rows unaligned (scalar path);
+    dim 6144 exceeds the register-resident path."""
+    print(f"[case] layernorm_mod rows={rows} dim={dim} offset={offset}", flush=True)
+    g = torch.Generator().manual_seed(rows + dim)
+    x = torch.randn(rows * dim + offset, generator=g) * 2 + 0.5
+    sc = torch.randn(dim, generator=g) * 0.3
+    sh = torch.randn(dim, generator=g)
+    xv = x[offset:].view(rows, dim)
+    ref = oracle.layernorm_mod(xv.numpy(), sc.numpy(), sh.numpy(), eps=1e-6)
+    xd = x.to(DEV)[offset:].view(rows, dim)
+    y32 = torch.empty(rows, dim, device=DEV)
+    kiln_amd.layernorm_mod(y32, xd, sc.to(DEV), sh.to(DEV), eps=1e-6)
+    y16 = torch.empty(rows, dim, dtype=torch.float16, device=DEV)
+    kiln_amd.layernorm_mod(y16, xd, sc.to(DEV), sh.to(DEV), eps=1e-6)
+    torch.cuda.synchronize()
+    d32 = np.abs(y32.cpu().numpy() - ref)
+    tol32 = 2e-5 * np.maximum(1.0, np.abs(ref))
+    print(f"[parity] layernorm_mod fp32: max-abs {d32.max():.3e}", flush=True)
+    assert (d32 <= tol32).all()
+    r16 = ref.astype(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(r16).astype(np.float16)).astype(np.float64)
+    d16 = np.abs(y16.cpu().numpy().astype(np.float64) - r16)
+    print(f"[parity] layernorm_mod16: max |diff| / (ulp + fp32 bar) {float((d16 / (ulp + tol32)).max()):.2f}",
+          flush=True)
+    assert (d16 <= ulp * 1.0001 + tol32).all()
+
+
+@pytest.mark.parametrize("rows,dim,gated", [(6912, 2048, True), (100, 2048, False), (33, 1001, True)])
+def test_add_gated(gpu, rows, dim, gated):
+    print(f"[case] add_gated rows={rows} dim={dim} gate={gated}", flush=True)
+    g = torch.Generator().manual_seed(rows * 3 + dim)
+    x = torch.randn(rows, dim, generator=g)
+    y = torch.randn(rows, dim, generator=g)
+    gate = torch.randn(dim, generator=g) if gated else None
+    ref = oracle.add_gated(x.numpy(), y.numpy(), gate.numpy() if gated else None)
+    xd = x.to(DEV)
+    kiln_amd.add_gated(xd, y.to(DEV), gate.to(DEV) if gated else None)
+    torch.cuda.synchronize()
+    d = np.abs(xd.cpu().numpy() - ref).max()
+    print(f"[parity] add_gated: max-abs {d:.3e}", flush=True)
+    assert d <= 1e-6 * max(1.0, float(np.abs(ref).max()))

@@ -217,3 +217,36 @@ def test_f16_rounding_matches_numpy():
                                   1e-5, np.inf, -np.inf, 0.1, 1 / 3], np.float32),
                         (rng.standard_normal(2000) * 1e-6).astype(np.float32)])
     np.testing.assert_array_equal(oracle.to_f16_bits(x), x.astype(np.float16).view(np.uint16))
+
+
+# ---- modulated LayerNorm and gated residual of the DiT block ----
+def test_layernorm_mod_matches_torch_float64():
+    """oracle.layernorm_mod against an independent float64 statement: torch layer_norm without affine,
+    then * (1 + scale) + shift (engine/src/kernels.cu:678-697)."""
+    rng = np.random.default_rng(7)
+    for rows, dim in [(3, 2048), (5, 1000), (2, 7)]:
+        x = (rng.standard_normal((rows, dim)) * 3 + 1.5).astype(np.float32)
+        sc = (rng.standard_normal(dim) * 0.2).astype(np.float32)
+        sh = rng.standard_normal(dim).astype(np.float32)
+        got = oracle.layernorm_mod(x, sc, sh, eps=1e-6)
+        ref = (torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (dim,), eps=1e-6)
+               * (1 + torch.from_numpy(sc).double()) + torch.from_numpy(sh).double()).numpy()
+        assert np.abs(got - ref).max() <= 2e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_layernorm_mod_unmodulated_is_standardized():
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((4, 512)) * 5 - 2).astype(np.float32)
+    y = oracle.layernorm_mod(x, np.zeros(512, np.float32), np.zeros(512, np.float32), eps=0.0).astype(np.float64)
+    assert np.abs(y.mean(axis=1)).max() < 1e-5
+    assert np.abs(y.var(axis=1) - 1).max() < 1e-4
+
+
+def test_add_gated_cases():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((3, 64)).astype(np.float32)
+    y = rng.standard_normal((3, 64)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.add_gated(x, y), x + y)
+    np.testing.assert_array_equal(oracle.add_gated(x, y, np.zeros(64, np.float32)), x)
+    g = np.arange(64, dtype=np.float32) / 8
+    np.testing.assert_allclose(oracle.add_gated(x, y, g), x + g[None, :] * y, rtol=0, atol=1e-6)

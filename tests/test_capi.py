@@ -73,6 +73,11 @@ def test_argument_validation_without_gpu(L):
     # dtype codes
     assert L.kiln_nag_combine(p, 8, p, 8, 7, 4, 8, 5.0, 2.5, 0.25, None) == kiln_amd.KILN_EINVAL
     assert L.kiln_kv_prepare(p, p, 2048, p, 2048, 3, 64, 16, None, 1e-6, None, None, None) == kiln_amd.KILN_EINVAL
+    # modulated LayerNorm / gated residual: sizes and null pointers
+    assert L.kiln_layernorm_mod(p, p, p, p, 4, 0, 1e-6, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_layernorm_mod16(p, p, None, p, 4, 2048, 1e-6, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_add_gated(p, None, None, 4, 2048, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_add_gated(p, p, None, -1, 2048, None) == kiln_amd.KILN_EINVAL
     # more batch items than one launch takes
     assert L.kiln_dit_self_attn_fused(p, 1, 2048, p, p, p, 1, 2048, None, None, 1e-6, None, None, 5, 64, 16, None, 0,
                                       None) != kiln_amd.KILN_OK

@@ -622,9 +622,10 @@ __global__ __launch_bounds__(256) void k_kv_prep(const PrepParams p) {
                 for (int cc = 0; cc < 2; cc++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) ss += x[cc][e] * x[cc][e];
-                ss += __shfl_xor(ss, 1);
-                ss += __shfl_xor(ss, 2);
-                ss += __shfl_xor(ss, 4);
+                // sum over the key's 8 consecutive lanes: DPP quad swaps, then the half-row mirror
+                ss += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0xB1, 0xF, 0xF, false));
+                ss += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x4E, 0xF, 0xF, false));
+                ss += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0x141, 0xF, 0xF, false));
                 const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
 #pragma unroll
                 for (int cc = 0; cc < 2; cc++)

@@ -261,21 +261,23 @@ __global__ __launch_bounds__(256) void k_nag_rows(T* a, int lda, const T* an, in
     if (row >= T_) return;
     T* p = a + (size_t)row * lda;
     const T* n = an + (size_t)row * ldn;
-    float pv[NAG_CH][8], g[NAG_CH][8];
+    float pv[NAG_CH][8], nv[NAG_CH][8], g[NAG_CH][8];
+    // all loads issued before any use (chunks past the row re-read its first chunk and are masked)
+#pragma unroll
+    for (int c = 0; c < NAG_CH; c++) {
+        const int i = (c * 64 + lane) * 8 < dim ? (c * 64 + lane) * 8 : 0;
+        load8(p + i, pv[c]);
+        load8(n + i, nv[c]);
+    }
     float lp = 0.f, lg = 0.f;
 #pragma unroll
     for (int c = 0; c < NAG_CH; c++) {
-        const int i = (c * 64 + lane) * 8;
-        if (i < dim) {
-            float nv[8];
-            load8(p + i, pv[c]);
-            load8(n + i, nv);
+        const bool in = (c * 64 + lane) * 8 < dim;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                g[c][e] = pv[c][e] * s - nv[e] * (s - 1.f);
-                lp += fabsf(pv[c][e]);
-                lg += fabsf(g[c][e]);
-            }
+        for (int e = 0; e < 8; e++) {
+            g[c][e] = pv[c][e] * s - nv[c][e] * (s - 1.f);
+            lp += in ? fabsf(pv[c][e]) : 0.f;
+            lg += in ? fabsf(g[c][e]) : 0.f;
         }
     }
     lp = wave_sum(lp);

@@ -236,6 +236,17 @@ def main():
     log(f"config 4 (T=4096, B=2): {ms4 * 1e3:.1f} us/call  {tf4:.1f} TFLOP/s  ({tf4 / PEAK_TFLOPS * 100:.1f}% peak); "
         f"attention kernel alone {ms4_main * 1e3:.1f} us  {tf4_main:.1f} TFLOP/s")
 
+    # one GPU's share of config 4 under 8-way head (tensor) parallelism: H = 2 of the 16 heads, same call
+    # (the first two heads of the same tensors); 128 workgroups, a quarter of the resident slots
+    h8 = 2
+    out8 = torch.empty_like(cfg4["q"])
+    ws8 = torch.empty(kiln_amd.dit_self_attn_workspace_bytes(2, cfg4["T"], h8), dtype=torch.uint8, device=dev)
+    ms_tp = tm.run(lambda: kiln_amd.dit_self_attn(out8, cfg4["q"], cfg4["k"], cfg4["v"], 2, cfg4["T"], h8, cfg4["qw"],
+                                                  cfg4["kw"], cfg4["rope"], workspace=ws8), args.steps, args.warmup)
+    tf_tp = cfg4["flop"] * h8 / H / ms_tp / 1e9
+    log(f"config 4, one GPU's share of 8-way head parallelism (H=2): {ms_tp * 1e3:.1f} us/call  {tf_tp:.1f} TFLOP/s")
+    del out8, ws8
+
     cfg2 = self_attn_case(torch, kiln_amd, 32, 48, 2, 2, dev)
     ms2 = tm.run(cfg2["step"], args.steps, args.warmup)
     tf2 = cfg2["flop"] / ms2 / 1e9
@@ -295,6 +306,8 @@ def main():
                         "QK-RMSNorm + 3D RoPE fused; step = K/V prepare + attention",
             "arch": arch,
             "pct_fp16_peak": round(tf4 / PEAK_TFLOPS * 100, 2),
+            "tp8_share_h2_ms_per_call": round(ms_tp, 5),
+            "tp8_share_h2_tflops": round(tf_tp, 2),
             "s1536_tflops": round(tf2, 2),
             "s1536_pct_fp16_peak": round(tf2 / PEAK_TFLOPS * 100, 2),
             "s1536_ms_per_call": round(ms2, 5),

@@ -144,6 +144,10 @@ int kiln_dit_self_attn_fused(void* out, int out_dtype, int ldo, const void* q, c
                              int in_dtype, int ld, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
                              const float* rope_cos, const float* rope_sin, int B, int T, int H, void* workspace,
                              size_t ws_bytes, kiln_stream_t stream);
+/* Workspace of kiln_dit_self_attn_fused on the current device: the prepared K/V of the B items, plus, when
+ * the launch would fill under a third of the device's workgroup slots (few heads, e.g. one GPU's share of a
+ * head-parallel run), the partial results of splitting every query tile's keys into ranges. A smaller
+ * workspace that still holds the prepared K/V runs the same call unsplit. */
 size_t kiln_dit_self_attn_workspace_bytes(int B, int T, int H);
 
 /* DiT cross-attention of a CFG batch plus NAG (engine/src/dit.cu:473-487): batch item b's queries

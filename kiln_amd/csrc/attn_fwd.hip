@@ -22,6 +22,7 @@
 //    tile's max exceeds it by more than 8 (log2 units), so P <= 2^8 stays far inside fp16 range.
 //  * 1-D grid with an XCD-aware block -> work mapping: consecutive work items (the query tiles of one
 //    head) land on the same XCD and share its L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -34,6 +35,8 @@ constexpr float RESCALE_TH = 8.0f;
 struct AttnParams {
     AttnJob job[MAX_JOBS];
     int njobs, Tq, H, ldq, ldo, qtiles, total, per;
+    int ksplit;   // key ranges per (query tile, head, job): > 1 writes partial (m, l, O) for k_attn_merge
+    float* part;  // partials: [unit][ksplit] x (O [128 rows][128] fp32, then (m, l) per row)
     int store_pairs;  // ldo or an output base not 8/16-byte aligned: store element pairs
     const uint16_t* qw;
     float eps, qscale;
@@ -76,13 +79,15 @@ __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
 // Work item of block b. Blocks are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8):
 // each XCD gets a contiguous range of work items, so the query tiles of one head share its L2.
 struct Work {
-    int qt, h, jb;
+    int qt, h, jb, ks;
 };
 __device__ __forceinline__ bool decode_work(const AttnParams& p, Work& w) {
     const int i = (int)(blockIdx.x & 7) * p.per + (int)(blockIdx.x >> 3);
     if (i >= p.total) return false;
     w.qt = i % p.qtiles;
-    const int rest = i / p.qtiles;
+    int rest = i / p.qtiles;
+    w.ks = rest % p.ksplit;  // the key ranges of one query tile sit in one XCD's range, next to each other
+    rest /= p.ksplit;
     w.h = rest % p.H;
     w.jb = rest / p.H;
     return true;
@@ -251,6 +256,7 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 typedef __attribute__((address_space(3))) half8 lds_half8;
 constexpr int QB = KILN_QB, NW = KILN_NW, NTHR = NW * 64, BM = NW * QB * 32, NS = KILN_NS;
 constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
+constexpr int PART_FLOATS = BM * HD + 2 * BM;      // one key range's partial result of a query tile
 static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
 static_assert(NW * QB == 4, "two workgroups of four 32-row blocks per CU");
 
@@ -272,7 +278,10 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     const AttnJob J = p.job[W.jb];
 
     const int Tk = J.Tk;
-    const int nh = (Tk + 31) / 32;  // half tiles holding real keys
+    const int nhall = (Tk + 31) / 32;  // half tiles holding real keys
+    // this unit's key range: half tiles [h0, h0 + nh) (all of them unless the launch splits the keys)
+    const int h0 = W.ks * nhall / p.ksplit;
+    const int nh = (W.ks + 1) * nhall / p.ksplit - h0;
     const _Float16* kvh = reinterpret_cast<const _Float16*>(J.kv) + (size_t)W.h * kv_head_stride(Tk);
     const uint32_t lds_base = (uint32_t)(size_t)(__attribute__((address_space(3))) _Float16*)lds;
 
@@ -289,7 +298,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         for (int i = 0; i < DMA_PER_HT; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc,
                                                      (__attribute__((address_space(3))) void*)(dst + i * NTHR * 8),
-                                                     16, dma_off, jh * (HT_H * 2) + i * (NTHR * 16), 0, 0);
+                                                     16, dma_off, (h0 + jh) * (HT_H * 2) + i * (NTHR * 16), 0, 0);
     };
     // operand reads through 32-bit LDS byte addresses: base + immediate offsets fold into ds_read_b128
     auto kptr = [&](int stage) {
@@ -448,7 +457,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 
 #pragma unroll
         for (int b = 0; b < QB; b++)
-            if constexpr (MASKN) mask_half(j + 1, Tk, hh, sn[b]);
+            if constexpr (MASKN) mask_half(h0 + j + 1, Tk, hh, sn[b]);
 #pragma unroll
         for (int db = 0; db < 4; db++)
 #pragma unroll
@@ -480,7 +489,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         for (int b = 0; b < QB; b++) sc[b] = sc2[b];
     }
     if (nh >= 2) {
-        if ((Tk & 31) != 0) step(True{}, j, sc, sc2);
+        if ((Tk & 31) != 0 && h0 + nh == nhall) step(True{}, j, sc, sc2);
         else step(False{}, j, sc, sc2);
         j++;
 #pragma unroll
@@ -516,7 +525,24 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     }
     KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is released
 #pragma unroll
-    for (int b = 0; b < QB; b++) epilogue<OutT>(p, J, row[b], qin[b], W.h, hh, m[b], l[b], o[b]);
+    for (int b = 0; b < QB; b++) {
+        if (p.ksplit > 1) {  // partial result of this key range: unnormalized O, running max m, row sum l
+            const int unit = (W.jb * p.H + W.h) * p.qtiles + W.qt;
+            float* po = p.part + (size_t)(unit * p.ksplit + W.ks) * PART_FLOATS;
+            const int r = (wv * QB + b) * 32 + (lane & 31);
+            float* prow = po + r * HD + 4 * hh;
+#pragma unroll
+            for (int db = 0; db < 4; db++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    *reinterpret_cast<floatx4*>(prow + db * 32 + 8 * g) =
+                        floatx4{o[b][db][4 * g], o[b][db][4 * g + 1], o[b][db][4 * g + 2], o[b][db][4 * g + 3]};
+            const float lt = pair_sum(l[b]);
+            if (hh == 0) *reinterpret_cast<float2*>(po + BM * HD + 2 * r) = make_float2(m[b], lt);
+        } else {
+            epilogue<OutT>(p, J, row[b], qin[b], W.h, hh, m[b], l[b], o[b]);
+        }
+    }
 #if KILN_CLOCK
     if (tid == 0 && blockIdx.x < 16384) {
         g_clk[blockIdx.x][0] = __builtin_amdgcn_s_memtime() - clk0;
@@ -678,17 +704,85 @@ __global__ __launch_bounds__(256) void k_kv_prep(const PrepParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// Merge of key-split partials (launches whose grid would fill under a quarter of the resident workgroup
+// slots split each unit's keys into ksplit ranges): per query row, O = sum_i O_i 2^(m_i - m) / sum_i l_i
+// 2^(m_i - m) with m = max_i m_i, then the npad zero keys and the output rounding of the epilogue.
+// ------------------------------------------------------------------------------------------------
+template <typename OutT>
+__global__ __launch_bounds__(256) void k_attn_merge(const AttnParams p) {
+    // block = 32 rows of one unit (four blocks per unit); thread = 16 columns of one row
+    const int unit = blockIdx.x >> 2, qt = unit % p.qtiles, rest = unit / p.qtiles, h = rest % p.H, jb = rest / p.H;
+    const AttnJob& J = p.job[jb];
+    const int r = (blockIdx.x & 3) * 32 + (threadIdx.x >> 3), c0 = 16 * (threadIdx.x & 7);
+    const int row = qt * BM + r;
+    if (row >= p.Tq) return;
+    const float* base = p.part + (size_t)unit * p.ksplit * PART_FLOATS;
+    float mx = -INFINITY;
+    for (int ks = 0; ks < p.ksplit; ks++) mx = fmaxf(mx, base[ks * PART_FLOATS + BM * HD + 2 * r]);
+    float lt = 0.f;
+    floatx4 acc[4] = {};
+    for (int ks = 0; ks < p.ksplit; ks++) {
+        const float* pk = base + ks * PART_FLOATS;
+        const float w = __builtin_amdgcn_exp2f(pk[BM * HD + 2 * r] - mx);
+        lt += pk[BM * HD + 2 * r + 1] * w;
+        const floatx4* src = reinterpret_cast<const floatx4*>(pk + r * HD + c0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] += src[i] * w;
+    }
+    float sc = 1.f;
+    if (J.npad) {
+        const float mn = fmaxf(mx, 0.f);
+        sc = __builtin_amdgcn_exp2f(mx - mn);
+        lt = lt * sc + (float)J.npad * __builtin_amdgcn_exp2f(-mn);
+    }
+    const float inv = sc / lt;
+    OutT* orow = reinterpret_cast<OutT*>(J.o) + (size_t)row * p.ldo + h * HD + c0;
+    const bool pairs = p.store_pairs != 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        store4<OutT>(orow + 4 * i, acc[i][0] * inv, acc[i][1] * inv, acc[i][2] * inv, acc[i][3] * inv, pairs);
+}
+
+// ------------------------------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------------------------------
+// resident workgroup slots of the current device (two per CU); 0 if there is no device
+static int resident_slots() {
+    static int slots[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!slots[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        slots[dev] = 2 * cus;
+    }
+    return slots[dev];
+}
+
+int attn_key_split(int njobs, int Tq, int Tk, int H) {
+    const long units = (long)((Tq + BM - 1) / BM) * H * njobs;
+    const int slots = resident_slots();
+    if (units <= 0 || slots <= 0) return 1;
+    long ks = slots / units;
+    ks = std::min<long>(ks, 8);
+    ks = std::min<long>(ks, ((Tk + 31) / 32) / 16);  // every range keeps at least 16 half tiles
+    return ks >= 3 ? (int)ks : 1;  // below 3 ranges the extra prologues and the merge cost more than they save
+}
+
+size_t attn_split_bytes(int ksplit, int njobs, int Tq, int H) {
+    if (ksplit <= 1) return 0;
+    return (size_t)((Tq + BM - 1) / BM) * H * njobs * ksplit * PART_FLOATS * sizeof(float);
+}
 template <typename InT, typename OutT, bool QN, bool RP>
 static hipError_t launch_sel(AttnParams p, int Tq, int units, hipStream_t s) {
     p.qtiles = (Tq + BM - 1) / BM;
-    p.total = p.qtiles * units;
+    p.total = p.qtiles * units * p.ksplit;
     const int nb = (p.total + 7) / 8 * 8;
     p.per = nb / 8;
     auto kern = k_attn_fwd<InT, OutT, QN, RP>;
     const size_t lds = (size_t)NS * HT_H * sizeof(_Float16);
     hipLaunchKernelGGL(kern, dim3(nb), dim3(NTHR), lds, s, p);
+    if (p.ksplit > 1) hipLaunchKernelGGL(k_attn_merge<OutT>, dim3(4 * p.qtiles * units), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
@@ -717,6 +811,8 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
     p.qscale = LOG2E / sqrtf((float)HD);
     p.rcos = a.rcos;
     p.rsin = a.rsin;
+    p.ksplit = a.part && a.ksplit > 1 ? a.ksplit : 1;
+    p.part = a.part;
     const bool qn = a.qw != nullptr, rp = a.rcos != nullptr;
     const int units = a.H * a.njobs;
     if (a.Tq <= 0 || units <= 0) return hipSuccess;

@@ -103,11 +103,19 @@ int flash_self(void* out, DT od, int ldo, long long bso, const void* q, int ldq,
     if (B <= 0 || B > kiln::MAX_JOBS) return fail(KILN_EUNSUPPORTED, "batch %d outside 1..%d", B, kiln::MAX_JOBS);
     const size_t per = kiln_kv_prepped_bytes(Tk, H);
     const size_t need = per * B;
+    // small grids split every unit's keys (partials behind the prepared K/V); a caller's workspace takes the
+    // split only if it is large enough for the partials too (the *_workspace_bytes functions that know Tq
+    // include them)
+    int ks = kiln::attn_key_split(B, Tq, Tk, H);
+    size_t split = kiln::attn_split_bytes(ks, B, Tq, H);
     if (!ws) {
-        int rc2 = get_workspace(need, &ws);
+        int rc2 = get_workspace(need + split, &ws);
         if (rc2) return rc2;
     } else if (ws_bytes < need) {
         return fail(KILN_ENOMEM, "workspace %zu bytes < %zu needed", ws_bytes, need);
+    } else if (ws_bytes < need + split) {
+        ks = 1;
+        split = 0;
     }
     const size_t isz = in == DT::F16 ? 2 : 4, osz = od == DT::F16 ? 2 : 4;
     kiln::AttnLaunch a{};
@@ -130,6 +138,8 @@ int flash_self(void* out, DT od, int ldo, long long bso, const void* q, int ldq,
     a.eps = eps;
     a.rcos = rc;
     a.rsin = rs;
+    a.ksplit = ks;
+    a.part = ks > 1 ? reinterpret_cast<float*>((char*)ws + need) : nullptr;
     return hip_check(kiln::launch_attn_fwd(a, stream), "attn_fwd launch");
 }
 
@@ -317,7 +327,9 @@ int kiln_attn_fwd_f16in(void* out, int out_dtype, int ldo, long long bso, const 
 }
 
 size_t kiln_dit_self_attn_workspace_bytes(int B, int T, int H) {
-    return B > 0 ? (size_t)B * kiln_kv_prepped_bytes(T, H) : 0;
+    if (B <= 0 || T <= 0 || H <= 0) return 0;
+    return (size_t)B * kiln_kv_prepped_bytes(T, H) +
+           kiln::attn_split_bytes(kiln::attn_key_split(B, T, T, H), B, T, H);
 }
 
 int kiln_dit_self_attn_fused(void* out, int out_dtype, int ldo, const void* q, const void* k, const void* v,

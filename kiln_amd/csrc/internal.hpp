@@ -27,7 +27,15 @@ struct AttnLaunch {
     float eps;
     const float* rcos;   // [Tq, 64] RoPE tables for Q or null
     const float* rsin;
+    int ksplit;          // > 1: split every unit's keys into ksplit ranges (partials in `part`, then a merge)
+    float* part;         // attn_split_bytes(ksplit, njobs, Tq, H) bytes of device scratch
 };
+
+// Key ranges per unit for a launch of njobs x H heads x Tq queries against Tk keys: > 1 only when the grid
+// would fill under a third of the resident workgroup slots (small head counts, one GPU's share of a
+// head-parallel run) and every range keeps at least 16 32-key half tiles.
+int attn_key_split(int njobs, int Tq, int Tk, int H);
+size_t attn_split_bytes(int ksplit, int njobs, int Tq, int H);
 
 hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s);
 

@@ -411,3 +411,59 @@ def test_add_gated(gpu, rows, dim, gated):
     d = np.abs(xd.cpu().numpy() - ref).max()
     print(f"[parity] add_gated: max-abs {d:.3e}", flush=True)
     assert d <= 1e-6 * max(1.0, float(np.abs(ref).max()))
+
+
+# ---- key-split launches (grids filling under a third of the workgroup slots) ----
+@pytest.mark.parametrize("Hh,Tq,Tk,npad", [(1, 512, 4096, 100), (1, 300, 3001, 0), (2, 130, 2048, 7)])
+def test_key_split_small_grid(gpu, Hh, Tq, Tk, npad):
+    """Few heads and queries against many keys: the launch splits each query tile's keys into ranges (up to
+    8, each >= 16 half tiles; Tk = 3001 ends on a ragged half tile) and merges the partials. Checked against
+    the double-accumulation oracle, through the fp32 drop-in (library workspace) with npad."""
+    print(f"[case] key split H={Hh} Tq={Tq} Tk={Tk} npad={npad}", flush=True)
+    g = torch.Generator().manual_seed(Tq + Tk)
+    q = torch.randn(Tq, Hh * D, generator=g)
+    k = torch.randn(Tk, Hh * D, generator=g)
+    v = torch.randn(Tk, Hh * D, generator=g)
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), Hh, npad=npad)
+    out = torch.full((Tq, Hh * D), float("nan"), dtype=torch.float32, device=DEV)
+    kiln_amd.attention(out, q.to(DEV), k.to(DEV), v.to(DEV), Tq, Tk, Hh, D, npad=npad)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, f"key split H={Hh} Tq={Tq} Tk={Tk} npad={npad}")
+
+
+def test_key_split_tp_share_config4(gpu):
+    """One GPU's share of config 4 under 8-way head parallelism (H=2 of 16, T=4096, B=2, QK-norm + RoPE,
+    fp16): 128 query-tile units, split 4 ways. Sampled query rows of both items against the oracle; the
+    caller's workspace sized by kiln_dit_self_attn_workspace_bytes (split) and one only large enough for
+    the prepared K/V (unsplit) give outputs within fp16 rounding of each other."""
+    Hh, B, Hp, Wp = 2, 2, 64, 64
+    T = Hp * Wp
+    print(f"[case] TP share H={Hh} T={T} B={B}", flush=True)
+    g = torch.Generator().manual_seed(77)
+    q, k, v = (torch.randn(B * T, Hh * D, generator=g).half() for _ in range(3))
+    qw = (torch.rand(D, generator=g) * 0.5 + 0.75).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=g) * 0.5 + 0.75).to(torch.bfloat16)
+    c, s = oracle.cosmos_rope(Hp, Wp)
+    rope = (torch.from_numpy(c).to(DEV), torch.from_numpy(s).to(DEV))
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    full = kiln_amd.dit_self_attn_workspace_bytes(B, T, Hh)
+    small = B * kiln_amd.kv_prepped_bytes(T, Hh)
+    assert full > small, "expected the split workspace on this device"
+    outs = []
+    for nbytes in (full, small):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        out = torch.empty(B * T, Hh * D, dtype=torch.float16, device=DEV)
+        kiln_amd.dit_self_attn(out, qd, kd, vd, B, T, Hh, qw.to(DEV), kw.to(DEV), rope, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(out.float().cpu().numpy())
+    qwb = qw.view(torch.int16).numpy().view(np.uint16)
+    kwb = kw.view(torch.int16).numpy().view(np.uint16)
+    rows = np.arange(0, T, 29)
+    for b in range(B):
+        sl = slice(b * T, (b + 1) * T)
+        qn = oracle.rope_half(oracle.rmsnorm_rows(q[sl].float().numpy(), qwb).reshape(T, Hh * D), Hh, c, s)
+        kn = oracle.rope_half(oracle.rmsnorm_rows(k[sl].float().numpy(), kwb).reshape(T, Hh * D), Hh, c, s)
+        ref = oracle.attn_f64(np.ascontiguousarray(qn[rows]), kn, v[sl].float().numpy(), Hh)
+        assert_close(outs[0][sl][rows], ref, f"TP share split, item {b}")
+        assert_close(outs[1][sl][rows], ref, f"TP share unsplit, item {b}")
+    assert np.abs(outs[0] - outs[1]).max() <= 2e-3

@@ -247,6 +247,15 @@ def main():
     log(f"config 4, one GPU's share of 8-way head parallelism (H=2): {ms_tp * 1e3:.1f} us/call  {tf_tp:.1f} TFLOP/s")
     del out8, ws8
 
+    # the unchanged-engine drop-in: attention16() with fp32 Q/K/V (already normed and roped, as the reference
+    # engine hands them over, engine/src/dit.cu:464-469), one call per CFG item at config 4's shape
+    qf, kf, vf = (t[:cfg4["T"]].float() for t in (cfg4["q"], cfg4["k"], cfg4["v"]))
+    o16 = torch.empty(cfg4["T"], H * D, dtype=torch.float16, device=dev)
+    ms_di = tm.run(lambda: kiln_amd.attention16(o16, qf, kf, vf, cfg4["T"], cfg4["T"], H), args.steps, args.warmup)
+    tf_di = cfg4["flop"] / 2 / ms_di / 1e9
+    log(f"drop-in attention16 (fp32 Q/K/V, one CFG item of config 4): {ms_di * 1e3:.1f} us/call  {tf_di:.1f} TFLOP/s")
+    del qf, kf, vf, o16
+
     cfg2 = self_attn_case(torch, kiln_amd, 32, 48, 2, 2, dev)
     ms2 = tm.run(cfg2["step"], args.steps, args.warmup)
     tf2 = cfg2["flop"] / ms2 / 1e9
@@ -306,6 +315,8 @@ def main():
                         "QK-RMSNorm + 3D RoPE fused; step = K/V prepare + attention",
             "arch": arch,
             "pct_fp16_peak": round(tf4 / PEAK_TFLOPS * 100, 2),
+            "dropin_attention16_f32in_ms_per_call": round(ms_di, 5),
+            "dropin_attention16_f32in_tflops": round(tf_di, 2),
             "tp8_share_h2_ms_per_call": round(ms_tp, 5),
             "tp8_share_h2_tflops": round(tf_tp, 2),
             "s1536_tflops": round(tf2, 2),

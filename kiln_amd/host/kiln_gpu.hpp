@@ -82,4 +82,85 @@ inline void nag16(uint16_t* a, const uint16_t* an, int T, int dim, float scale, 
           "nag");
 }
 
+// ---- the DiT block's attention section (engine/src/dit.cu:458-488) and its per-generation state ----
+
+// Cross-attention context of one generation: the reference's Dit::Context (rows [real, len) are zero padding,
+// engine/src/models.h:26) together with its Dit::KVCache (models.h:56-58): every block's K/V, prepared once by
+// prepare() (Dit::cache_context, engine/src/dit.cu:217-234) in the attention kernel's tiled layout. The padding
+// rows are never stored: they enter the softmax analytically as npad = len - real zero keys.
+class ContextKV {
+   public:
+    ContextKV(int nblocks, int len, int real, int H) : nblocks_(nblocks), len_(len), real_(real), H_(H) {
+        if (nblocks <= 0 || real <= 0 || len < real || H <= 0) throw std::runtime_error("ContextKV: bad sizes");
+        per_ = kiln_kv_prepped_bytes(real, H);
+        if (hipMalloc(&buf_, per_ * nblocks) != hipSuccess) throw std::runtime_error("ContextKV: hipMalloc failed");
+    }
+    ~ContextKV() {
+        if (buf_) (void)hipFree(buf_);
+    }
+    ContextKV(const ContextKV&) = delete;
+    ContextKV& operator=(const ContextKV&) = delete;
+
+    // block i's raw context projections K, V [real, ld] (in_dtype KILN_F32 or KILN_F16, head h at column
+    // h*128); K is RMS-normed per head with the bf16 weights k_norm_w (null: no norm).
+    void prepare(int block, const void* k, const void* v, int ld, int in_dtype, const uint16_t* k_norm_w, float eps) {
+        if (block < 0 || block >= nblocks_) throw std::runtime_error("ContextKV::prepare: block out of range");
+        check(kiln_kv_prepare(kv_mut(block), k, ld, v, ld, in_dtype, real_, H_, k_norm_w, eps, nullptr, nullptr,
+                              (kiln_stream_t)stream_ref()),
+              "cache_context");
+    }
+    const uint16_t* kv(int block) const { return reinterpret_cast<const uint16_t*>((const char*)buf_ + per_ * block); }
+    int len() const { return len_; }
+    int real() const { return real_; }
+    int npad() const { return len_ - real_; }
+    int heads() const { return H_; }
+
+   private:
+    uint16_t* kv_mut(int block) { return reinterpret_cast<uint16_t*>((char*)buf_ + per_ * block); }
+    int nblocks_, len_, real_, H_;
+    size_t per_ = 0;
+    void* buf_ = nullptr;
+};
+
+// Normalized Attention Guidance settings of the reference (Dit::Nag, engine/src/models.h:80): with `neg` set,
+// batch item 0's cross-attention output becomes the NAG blend of its positive and negative attentions.
+struct Nag {
+    const ContextKV* neg = nullptr;
+    float scale = 5.f, tau = 2.5f, alpha = 0.25f;
+};
+
+// Self-attention of a CFG batch (engine/src/dit.cu:458-470): raw projections q, k, v [B*T, ld] (item b at
+// rows b*T), QK-RMSNorm with bf16 weights and RoPE tables [T, 64] applied inside, fp16 out [B*T, ldo].
+// ws may be null (library-owned workspace) or kiln_dit_self_attn_workspace_bytes(B, T, H) bytes.
+inline void dit_self_attention(uint16_t* out, int ldo, const void* q, const void* k, const void* v, int in_dtype,
+                               int ld, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                               const float* rope_cos, const float* rope_sin, int B, int T, int H, void* ws = nullptr,
+                               size_t ws_bytes = 0) {
+    check(kiln_dit_self_attn_fused(out, KILN_F16, ldo, q, k, v, in_dtype, ld, q_norm_w, k_norm_w, eps, rope_cos,
+                                   rope_sin, B, T, H, ws, ws_bytes, (kiln_stream_t)stream_ref()),
+          "self-attention");
+}
+
+// Cross-attention of a CFG batch for block `block` (engine/src/dit.cu:473-487): item b's queries (rows b*T of
+// q, RMS-normed inside with q_norm_w) attend to cs[b]; with nag.neg, item 0 also attends to the negative
+// context into out_neg [T, ldo] (caller scratch) and its output becomes the NAG blend.
+inline void dit_cross_attention(uint16_t* out, uint16_t* out_neg, int ldo, const void* q, int in_dtype, int ldq,
+                                const uint16_t* q_norm_w, float eps, int B, int T, int H, int block,
+                                const ContextKV* const* cs, const Nag& nag = Nag()) {
+    if (B <= 0 || B > 3) throw std::runtime_error("dit_cross_attention: B outside 1..3");
+    const uint16_t* kvp[3];
+    int Lk[3], np[3];
+    for (int b = 0; b < B; b++) {
+        if (cs[b]->heads() != H) throw std::runtime_error("dit_cross_attention: context prepared for other heads");
+        kvp[b] = cs[b]->kv(block);
+        Lk[b] = cs[b]->real();
+        np[b] = cs[b]->npad();
+    }
+    const ContextKV* n = nag.neg;
+    check(kiln_cross_attn_nag(out, out_neg, KILN_F16, ldo, q, in_dtype, ldq, q_norm_w, eps, B, T, H, kvp, Lk, np,
+                              n ? n->kv(block) : nullptr, n ? n->real() : 0, n ? n->npad() : 0, nag.scale, nag.tau,
+                              nag.alpha, (kiln_stream_t)stream_ref()),
+          "cross-attention");
+}
+
 }  // namespace kiln

@@ -43,6 +43,24 @@ def _cases(n=24, seed=2024):
 CASES = _cases()
 
 
+def _split_cases(n=8, seed=77):
+    """Few heads and queries against long key sequences: grids under a third of the workgroup slots, so the
+    launch splits every query tile's keys into ranges and merges the partials (fp32/fp16 drop-ins and the
+    batched fp16 entry point with the library's workspace)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        route = ["f32out", "f16out", "f16in"][i % 3]
+        out.append(dict(route=route, H=int(rng.choice([1, 2])), pad=[int(rng.choice([0, 8, 24])) for _ in range(4)],
+                        off=int(rng.choice([0, 8])), seed=5000 + i, Tq=int(rng.integers(1, 400)),
+                        Tk=int(rng.integers(1500, 5000)), npad=int(rng.choice([0, int(rng.integers(1, 300))])),
+                        B=int(rng.integers(1, 3)), out32=bool(rng.integers(0, 2)), causal=False))
+    return out
+
+
+SPLIT_CASES = _split_cases()
+
+
 def _strided(rows, H, pad, off, dtype, data):
     """[rows, H*D] view of a [rows, off + H*D + pad] buffer (row stride = off + H*D + pad), holding data."""
     buf = torch.zeros(rows, off + H * D + pad, dtype=dtype, device=DEV)
@@ -54,7 +72,15 @@ def _strided(rows, H, pad, off, dtype, data):
 
 @pytest.mark.parametrize("idx", range(len(CASES)))
 def test_random_shapes(gpu, idx):
-    c = CASES[idx]
+    _run_case(CASES[idx], idx)
+
+
+@pytest.mark.parametrize("idx", range(len(SPLIT_CASES)))
+def test_random_split_shapes(gpu, idx):
+    _run_case(SPLIT_CASES[idx], 100 + idx)
+
+
+def _run_case(c, idx):
     H, pad, off = c["H"], c["pad"], c["off"]
     g = torch.Generator().manual_seed(c["seed"])
     print(f"[random] case {idx}: {c}", flush=True)

@@ -262,6 +262,23 @@ def main():
     log(f"config 2 (T=1536, B=2): {ms2 * 1e3:.1f} us/call  {tf2:.1f} TFLOP/s  ({tf2 / PEAK_TFLOPS * 100:.1f}% peak)")
     del cfg2
 
+    # config 3: text cross-attention with NAG, 1536 queries (QK-normed) over a positive and a negative
+    # 512-token context (prepared once per generation, outside the call), NAG combine of the two outputs
+    T3, L3 = 1536, 512
+    g3 = torch.Generator(device=dev).manual_seed(3)
+    q3 = torch.randn(T3, H * D, generator=g3, device=dev).half()
+    w3 = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    ctx3 = [kiln_amd.kv_prepare(torch.randn(L3, H * D, generator=g3, device=dev).half(),
+                                torch.randn(L3, H * D, generator=g3, device=dev).half(), H, k_norm_w=w3)
+            for _ in range(2)]
+    o3 = torch.empty(T3, H * D, dtype=torch.float16, device=dev)
+    n3 = torch.empty(T3, H * D, dtype=torch.float16, device=dev)
+    ms3 = tm.run(lambda: kiln_amd.cross_attn_nag(o3, q3, 1, T3, H, ctx3[:1], [L3], [0], q_norm_w=w3, kvp_neg=ctx3[1],
+                                                 Lk_neg=L3, npad_neg=0, out_neg=n3), args.steps, args.warmup)
+    tf3 = 2 * 4.0 * H * T3 * L3 * D / ms3 / 1e9
+    log(f"config 3 (cross-attention 1536 x 512, positive + negative + NAG): {ms3 * 1e3:.1f} us/call  {tf3:.1f} TFLOP/s")
+    del q3, ctx3, o3, n3
+
     cfg5 = dit_step_case(torch, kiln_amd, dev)
     ms5 = tm.run(cfg5["step"], max(3, args.steps // 4), max(1, args.warmup // 2))
     log(f"config 5 (T=3456, 28 blocks, self + cross + NAG): {ms5:.3f} ms attention per DiT step  "
@@ -322,6 +339,8 @@ def main():
             "s1536_tflops": round(tf2, 2),
             "s1536_pct_fp16_peak": round(tf2 / PEAK_TFLOPS * 100, 2),
             "s1536_ms_per_call": round(ms2, 5),
+            "cross_nag_1536x512_ms_per_call": round(ms3, 5),
+            "cross_nag_1536x512_tflops": round(tf3, 2),
             "dit_step_attention_ms": round(ms5, 4),
             "dit_step_workload": "config 5: 768x1152 (T=3456), B=2, 28 blocks x (self + cross L=512 + NAG)",
             "layernorm_mod16_us": round(ms_ln * 1e3, 2),

@@ -22,6 +22,8 @@
 //    tile's max exceeds it by more than 8 (log2 units), so P <= 2^8 stays far inside fp16 range.
 //  * 1-D grid with an XCD-aware block -> work mapping: consecutive work items (the query tiles of one
 //    head) land on the same XCD and share its L2.
+//  * grids that would fill under a third of the resident workgroup slots split every query tile's keys into
+//    ranges; each range writes a partial (unnormalized O, m, l) and k_attn_merge combines them.
 #include <algorithm>
 #include <type_traits>
 

@@ -130,7 +130,9 @@ int kiln_attn_fwd_prepped_batch(void* out, int out_dtype, int ldo, long long bso
                                 const float* rope_sin, const uint16_t* const* kvp, int B, int Tq, int Tk, int H,
                                 int npad, kiln_stream_t stream);
 
-/* Plain batched fp16 attention: B independent (Q, K, V) sets at batch strides bs* (elements). */
+/* Plain batched fp16 attention: B independent (Q, K, V) sets at batch strides bs* (elements).
+ * workspace NULL = library-owned (sized for the key split of small grids too); a caller's workspace of
+ * kiln_attn_fwd_f16in_workspace_bytes() runs unsplit. */
 int kiln_attn_fwd_f16in(void* out, int out_dtype, int ldo, long long bso, const uint16_t* q, int ldq, long long bsq,
                         const uint16_t* k, int ldk, long long bsk, const uint16_t* v, int ldv, long long bsv, int B,
                         int Tq, int Tk, int H, int npad, void* workspace, size_t ws_bytes, kiln_stream_t stream);

@@ -330,8 +330,8 @@ hipError_t launch_nag(void* a, int lda, const void* an, int ldn, DT dt, int T, i
 // causal limit key <= query, with npad the max starts at 0 and npad*exp(-m) joins the denominator.
 constexpr int EX_CH = 256;
 __global__ __launch_bounds__(256) void k_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k,
-                                                    int ldk, const float* v, int ldv, int Tk, int H, int Dh,
-                                                    int causal, int npad, float scale) {
+                                                    int ldk, const float* v, int ldv, int Tk, int Dh, int causal,
+                                                    int npad, float scale) {
     __shared__ float qs[256];
     __shared__ float ps[EX_CH];
     __shared__ float red[4];
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void k_exact_attn(float* out, int ldo, const f
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s) {
     if (Tq <= 0 || H <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_exact_attn, dim3(Tq, H), dim3(256), 0, s, out, ldo, q, ldq, k, ldk, v, ldv, Tk, H, Dh,
+    hipLaunchKernelGGL(k_exact_attn, dim3(Tq, H), dim3(256), 0, s, out, ldo, q, ldq, k, ldk, v, ldv, Tk, Dh,
                        causal ? 1 : 0, npad, 1.f / sqrtf((float)Dh));
     return hipGetLastError();
 }

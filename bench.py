@@ -97,26 +97,39 @@ def self_attn_case(torch, kiln_amd, Hp, Wp, B, seed, dev):
                 rope=rope)
 
 
+def linear_init(torch, out_f, in_f, g, dev):
+    """torch.nn.Linear's default weight init: U(+-1/sqrt(in_features))."""
+    return (torch.rand(out_f, in_f, generator=g, device=dev) * 2 - 1) / in_f ** 0.5
+
+
+def context_kv(torch, kiln_amd, L, g, dev, kw, emb_dim=1024):
+    """One prepared cross-attention context: N(0,1) text embeddings [L, 1024] (Qwen3-0.6B-sized) projected to
+    2048 by random-init K/V weights, K RMS-normed (Dit::cache_context, engine/src/dit.cu:217-234)."""
+    e = torch.randn(L, emb_dim, generator=g, device=dev)
+    kk = (e @ linear_init(torch, H * D, emb_dim, g, dev).T).half()
+    vv = (e @ linear_init(torch, H * D, emb_dim, g, dev).T).half()
+    return kiln_amd.kv_prepare(kk, vv, H, k_norm_w=kw)
+
+
 def dit_step_case(torch, kiln_amd, dev, nblocks=28, Hp=48, Wp=72, B=2, L=512, seed=100):
     """Attention of a full DiT denoising step at 768x1152 (T=3456): per block, self-attention of the CFG pair
     (QK-norm + RoPE) and cross-attention of each item against its cached context, plus the NAG negative
-    attention of item 0 and the NAG combine (engine/src/dit.cu:458-488). Context K/V are prepared once per
-    generation (Dit::cache_context, engine/src/dit.cu:217-234) and are outside the step."""
+    attention of item 0 and the NAG combine (engine/src/dit.cu:458-488). Every block's Q/K/V and cross-attention
+    Q are projections of N(0,1) activations by its own random-init 2B-shaped weights (computed at set-up, not
+    timed); the three contexts (positive, unconditional, NAG negative) are projections of 1024-d embeddings,
+    prepared once per generation (Dit::cache_context, engine/src/dit.cu:217-234) and outside the step."""
     T = Hp * Wp
     c, s = kiln_amd.cosmos_rope_tables(Hp, Wp)
     rope = (c.to(dev), s.to(dev))
-    qw = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    qw = torch.ones(D, dtype=torch.bfloat16, device=dev)  # torch RMSNorm init
     g = torch.Generator(device=dev).manual_seed(seed)
     blocks = []
     ws = torch.empty(kiln_amd.dit_self_attn_workspace_bytes(B, T, H), dtype=torch.uint8, device=dev)
     for i in range(nblocks):
-        q, k, v = (torch.randn(B * T, H * D, generator=g, device=dev).half() for _ in range(3))
-        qc = torch.randn(B * T, H * D, generator=g, device=dev).half()
-        ctx = []
-        for _ in range(3):  # positive, uncond (CFG item 1), NAG negative
-            kk = torch.randn(L, H * D, generator=g, device=dev).half()
-            vv = torch.randn(L, H * D, generator=g, device=dev).half()
-            ctx.append(kiln_amd.kv_prepare(kk, vv, H, k_norm_w=qw))
+        X = torch.randn(B * T, H * D, generator=g, device=dev)
+        q, k, v, qc = ((X @ linear_init(torch, H * D, H * D, g, dev).T).half() for _ in range(4))
+        del X
+        ctx = [context_kv(torch, kiln_amd, L, g, dev, qw) for _ in range(3)]
         blocks.append((q, k, v, qc, ctx))
     a_self = torch.empty(B * T, H * D, dtype=torch.float16, device=dev)
     a_cross = torch.empty(B * T, H * D, dtype=torch.float16, device=dev)
@@ -262,15 +275,14 @@ def main():
     log(f"config 2 (T=1536, B=2): {ms2 * 1e3:.1f} us/call  {tf2:.1f} TFLOP/s  ({tf2 / PEAK_TFLOPS * 100:.1f}% peak)")
     del cfg2
 
-    # config 3: text cross-attention with NAG, 1536 queries (QK-normed) over a positive and a negative
-    # 512-token context (prepared once per generation, outside the call), NAG combine of the two outputs
+    # config 3: text cross-attention with NAG, 1536 queries (projected, RMS-normed in the call) over a positive
+    # and a negative 512-token context (1024-d embeddings projected to 2048, prepared once per generation,
+    # outside the call), NAG combine of the two outputs
     T3, L3 = 1536, 512
     g3 = torch.Generator(device=dev).manual_seed(3)
-    q3 = torch.randn(T3, H * D, generator=g3, device=dev).half()
+    q3 = (torch.randn(T3, H * D, generator=g3, device=dev) @ linear_init(torch, H * D, H * D, g3, dev).T).half()
     w3 = torch.ones(D, dtype=torch.bfloat16, device=dev)
-    ctx3 = [kiln_amd.kv_prepare(torch.randn(L3, H * D, generator=g3, device=dev).half(),
-                                torch.randn(L3, H * D, generator=g3, device=dev).half(), H, k_norm_w=w3)
-            for _ in range(2)]
+    ctx3 = [context_kv(torch, kiln_amd, L3, g3, dev, w3) for _ in range(2)]
     o3 = torch.empty(T3, H * D, dtype=torch.float16, device=dev)
     n3 = torch.empty(T3, H * D, dtype=torch.float16, device=dev)
     ms3 = tm.run(lambda: kiln_amd.cross_attn_nag(o3, q3, 1, T3, H, ctx3[:1], [L3], [0], q_norm_w=w3, kvp_neg=ctx3[1],

@@ -97,6 +97,23 @@ int kiln_layernorm_mod16(uint16_t* y, const float* x, const float* scale, const 
  * x += gate * y per row (gate fp32 [dim], NULL = 1). x, y [rows, dim] dense fp32. */
 int kiln_add_gated(float* x, const float* y, const float* gate, int rows, int dim, kiln_stream_t stream);
 
+/* Epilogues of kiln_linear16: the reference's Epi16 (engine/src/gpu.h:125, tcgemm16.cuh:20). */
+typedef enum { KILN_EPI_F32 = 0, KILN_EPI_F16 = 1, KILN_EPI_GELU16 = 2, KILN_EPI_RESID = 3 } kiln_epi;
+
+/* Replaces linear16() (engine/src/gpu.h:126, impl engine/src/kernels.cu:573-609 with tc16::k_gemm16,
+ * engine/src/tcgemm16.cuh:1-200): acc = x16 W^T over x16 fp16 [T, cols] (dense rows) and the fp16 weight
+ * W [rows, cols] (a weight after weight_to_f16), plus the folded LoRA product a2 w2^T (a2 fp16 [T, k2],
+ * w2 fp16 [rows, k2], dense; k2 = 0: none), accumulated in fp32. Epilogue by `epi`:
+ *   KILN_EPI_F32:    y fp32  = acc + beta*y
+ *   KILN_EPI_F16:    y fp16  = acc
+ *   KILN_EPI_GELU16: y fp16  = GELU(acc) = acc/2 (1 + erf(acc/sqrt 2))
+ *   KILN_EPI_RESID:  y fp32 += gate[col] * acc   (gate fp32 [rows], NULL = 1)
+ * y has rows of ldy >= rows elements. Requires rows % 128 == 0, cols % 32 == 0, k2 % 32 == 0 (the reference's
+ * eligibility, tcgemm16.cuh:177) and 16-byte aligned x16/W/a2/w2 (KILN_EUNSUPPORTED otherwise, where the
+ * reference throws); ldy even and y aligned to two elements. */
+int kiln_linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows, int cols, int epi,
+                  const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2, kiln_stream_t stream);
+
 /* Host-side Cosmos 3D RoPE tables for an Hp x Wp patch grid (engine/src/dit.cu:196-215):
  * cos_t, sin_t are HOST arrays of Hp*Wp*64 floats. */
 int kiln_cosmos_rope_tables(float* cos_t, float* sin_t, int Hp, int Wp);

@@ -19,6 +19,7 @@ HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "kiln_attn.h")
 
 KILN_OK, KILN_EINVAL, KILN_EUNSUPPORTED, KILN_EHIP, KILN_ENOMEM = 0, 1, 2, 3, 4
 KILN_F32, KILN_F16 = 0, 1
+KILN_EPI_F32, KILN_EPI_F16, KILN_EPI_GELU16, KILN_EPI_RESID = 0, 1, 2, 3
 
 _i, _ll, _f, _vp, _sz = ctypes.c_int, ctypes.c_longlong, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
 
@@ -35,6 +36,7 @@ _SIGS = {
     "kiln_layernorm_mod": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "kiln_layernorm_mod16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "kiln_add_gated": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "kiln_linear16": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "kiln_nag_combine": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _f, _f, _f, _vp]),
     "kiln_cosmos_rope_tables": (_i, [_vp, _vp, _i, _i]),
     "kiln_kv_prepped_bytes": (_sz, [_i, _i]),
@@ -269,3 +271,16 @@ def cross_attn_nag(out, q, B, T, H, kvps, Lks, npads, q_norm_w=None, eps=1e-6, k
                                      ctypes.cast(lks, _vp), ctypes.cast(nps, _vp), _ptr(kvp_neg), Lk_neg, npad_neg,
                                      scale, tau, alpha, _stream(stream)))
     return out
+
+
+def linear16(y, x16, w16, epi=KILN_EPI_F32, gate=None, beta=0.0, a2=None, w2=None, stream=None):
+    """linear16() (engine/src/kernels.cu:573-609): acc = x16 w16^T (+ a2 w2^T) with epilogue `epi`.
+
+    x16 fp16 [T, cols], w16 fp16 [rows, cols], y [T, >= rows] (fp32 for F32/RESID, fp16 for F16/GELU16,
+    row stride y.stride(0)); a2 [T, k2] / w2 [rows, k2] fp16 or None."""
+    T, cols = x16.shape
+    rows = w16.shape[0]
+    k2 = 0 if a2 is None else a2.shape[1]
+    _check(lib().kiln_linear16(_ptr(y), y.stride(0), _ptr(x16), T, _ptr(w16), rows, cols, epi, _ptr(gate), beta,
+                               _ptr(a2), _ptr(w2), k2, _stream(stream)))
+    return y

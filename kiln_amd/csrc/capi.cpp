@@ -421,6 +421,38 @@ int kiln_add_gated(float* x, const float* y, const float* gate, int rows, int di
     return hip_check(kiln::launch_add_gated(x, y, gate, rows, dim, (hipStream_t)stream), "add_gated launch");
 }
 
+int kiln_linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows, int cols, int epi,
+                  const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2, kiln_stream_t stream) {
+    if (epi < KILN_EPI_F32 || epi > KILN_EPI_RESID) return fail(KILN_EINVAL, "linear16: epilogue %d", epi);
+    if (T < 0 || rows <= 0 || cols <= 0 || k2 < 0)
+        return fail(KILN_EINVAL, "linear16: bad sizes T=%d rows=%d cols=%d k2=%d", T, rows, cols, k2);
+    if (rows % 128 || cols % 32 || k2 % 32)
+        return fail(KILN_EUNSUPPORTED, "linear16: needs rows %% 128 == 0, cols %% 32 == 0, k2 %% 32 == 0 (rows=%d cols=%d k2=%d)",
+                    rows, cols, k2);
+    if (ldy < rows) return fail(KILN_EINVAL, "linear16: ldy=%d < rows=%d", ldy, rows);
+    if (T == 0) return KILN_OK;
+    if (!y || !x16 || !w16 || (k2 && (!a2 || !w2))) return fail(KILN_EINVAL, "linear16: null pointer");
+    if (!aligned16(x16) || !aligned16(w16) || (k2 && (!aligned16(a2) || !aligned16(w2))))
+        return fail(KILN_EUNSUPPORTED, "linear16: operands must be 16-byte aligned");
+    const size_t esz = (epi == KILN_EPI_F32 || epi == KILN_EPI_RESID) ? 4 : 2;
+    if (ldy % 2 || (size_t)y % (2 * esz)) return fail(KILN_EUNSUPPORTED, "linear16: y rows must hold element pairs");
+    kiln::GemmLaunch g;
+    g.a = x16;
+    g.w = w16;
+    g.K = cols;
+    g.a2 = a2;
+    g.w2 = w2;
+    g.K2 = k2;
+    g.c = y;
+    g.ldc = ldy;
+    g.gate = gate;
+    g.beta = beta;
+    g.M = T;
+    g.N = rows;
+    g.epi = epi;
+    return hip_check(kiln::launch_gemm16(g, (hipStream_t)stream), "linear16 launch");
+}
+
 int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {
     if (T < 0 || H <= 0 || Dh <= 0 || Dh % 2) return fail(KILN_EINVAL, "bad sizes");
     if (T && (!x || !cos_t || !sin_t)) return fail(KILN_EINVAL, "null pointer");

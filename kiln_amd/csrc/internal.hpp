@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/kiln_attn.h"
+
 namespace kiln {
 
 enum class DT { F32 = 0, F16 = 1 };
@@ -50,6 +52,24 @@ struct KVPrepJob {
 // Prepares njobs (<= MAX_JOBS) contexts of Tk keys and H heads in one launch (K RMSNorm with kw, RoPE).
 hipError_t launch_kv_prep(const KVPrepJob* jobs, int njobs, DT in, int Tk, int H, const uint16_t* kw, float eps,
                           const float* rcos, const float* rsin, hipStream_t s);
+
+// acc = a [M,K] w[N,K]^T (+ a2 [M,K2] w2[N,K2]^T), all fp16 dense rows; epilogue `epi` (kiln_epi) into c (row
+// stride ldc). N % 128 == 0, K % 32 == 0, K2 % 32 == 0, 16-byte aligned operand bases.
+struct GemmLaunch {
+    const uint16_t* a;
+    const uint16_t* w;
+    int K;
+    const uint16_t* a2;
+    const uint16_t* w2;
+    int K2;
+    void* c;
+    int ldc;
+    const float* gate;
+    float beta;
+    int M, N;
+    int epi;
+};
+hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s);
 
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s);

@@ -32,6 +32,8 @@ def lib():
         L.oracle_rmsnorm_rows.argtypes = [_f32p, _f32p, ctypes.c_void_p, ctypes.c_long, _i, ctypes.c_float]
         L.oracle_layernorm_mod.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_long, _i, ctypes.c_float]
         L.oracle_add_gated.argtypes = [_f32p, _f32p, ctypes.c_void_p, ctypes.c_long, _i]
+        L.oracle_linear16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _i, _u16p, _i, _u16p, _i, _i, ctypes.c_void_p,
+                                      ctypes.c_void_p, _i, _i, ctypes.c_void_p, ctypes.c_float]
         L.oracle_rope_half.argtypes = [_f32p, _i, _i, _i, _i, _f32p, _f32p]
         L.oracle_cosmos_rope.argtypes = [_f32p, _f32p, _i, _i]
         L.oracle_nag.argtypes = [_f32p, _i, _f32p, _i, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float]
@@ -93,6 +95,35 @@ def add_gated(x, y, gate=None):
     y = _c32(y)
     g = _c32(gate) if gate is not None else None
     lib().oracle_add_gated(out, y, g.ctypes.data if g is not None else None, out.shape[0], out.shape[1])
+    return out
+
+
+EPI_F32, EPI_F16, EPI_GELU16, EPI_RESID = 0, 1, 2, 3
+
+
+def linear16(x16, w16, epi=EPI_F32, y=None, gate=None, beta=0.0, a2=None, w2=None):
+    """linear16 (engine/src/kernels.cu:573-609, epilogue tcgemm16.cuh:145-175) over fp16 bit patterns (uint16).
+
+    x16 [T, cols], w16 [rows, cols], a2 [T, k2] / w2 [rows, k2] or None. F32/RESID: y is the fp32 [T, rows] input
+    (zeros if None) and the result is a new fp32 array; F16/GELU16: returns fp16 bit patterns [T, rows]."""
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    w16 = np.ascontiguousarray(w16, dtype=np.uint16)
+    T, cols = x16.shape
+    rows = w16.shape[0]
+    k2 = 0
+    if a2 is not None:
+        a2 = np.ascontiguousarray(a2, dtype=np.uint16)
+        w2 = np.ascontiguousarray(w2, dtype=np.uint16)
+        k2 = a2.shape[1]
+    if epi in (EPI_F32, EPI_RESID):
+        out = _c32(y).copy() if y is not None else np.zeros((T, rows), np.float32)
+        o32, o16 = out.ctypes.data, None
+    else:
+        out = np.zeros((T, rows), np.uint16)
+        o32, o16 = None, out.ctypes.data
+    g = _c32(gate) if gate is not None else None
+    lib().oracle_linear16(o32, o16, rows, x16, T, w16, rows, cols, a2.ctypes.data if k2 else None,
+                          w2.ctypes.data if k2 else None, k2, epi, g.ctypes.data if g is not None else None, beta)
     return out
 
 

@@ -297,6 +297,44 @@ void oracle_add_gated(float* x, const float* y, const float* gate, long rows, in
 }
 
 /*
+ * fp16 linear layer with fused epilogue (engine/src/kernels.cu:573-609 linear16, kernel tc16::k_gemm16 with its
+ * epilogue at engine/src/tcgemm16.cuh:145-175):
+ *   acc[t][n] = sum_k x16[t][k] w16[n][k] + sum_k a2[t][k] w2[n][k]      (k2 = 0: no second product)
+ * accumulated in double over the exact fp16 values, then by epi:
+ *   0 F32:    y32[t][n] = acc + beta * y32[t][n]
+ *   1 F16:    y16[t][n] = fp16(acc)
+ *   2 GELU16: y16[t][n] = fp16(acc/2 (1 + erf(acc/sqrt 2)))      (the erf form, tcgemm16.cuh:55)
+ *   3 RESID:  y32[t][n] = y32[t][n] + (gate ? gate[n] : 1) * acc
+ * y rows have ldy elements. The reference accumulates 32-wide k tiles in fp16 (tcgemm16.cuh:6-7); the oracle is
+ * the exact sum, which both the reference and the GPU path approximate.
+ * Pinned: equals numpy float64 x @ w.T (+ a2 @ w2.T) on the same fp16 values; the LoRA product equals one
+ * product over the concatenated [x | a2] and [w | w2]; GELU equals math.erf's closed form, with GELU(0) = 0 and
+ * GELU(v) -> v for large v; RESID with gate = 0 leaves y unchanged.
+ */
+void oracle_linear16(float* y32, uint16_t* y16, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows,
+                     int cols, const uint16_t* a2, const uint16_t* w2, int k2, int epi, const float* gate, float beta) {
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; t++) {
+        double* xr = (double*)malloc(sizeof(double) * (size_t)(cols + k2));
+        for (int k = 0; k < cols; k++) xr[k] = f16_to_f32(x16[(size_t)t * cols + k]);
+        for (int k = 0; k < k2; k++) xr[cols + k] = f16_to_f32(a2[(size_t)t * k2 + k]);
+        for (int n = 0; n < rows; n++) {
+            double acc = 0.0;
+            for (int k = 0; k < cols; k++) acc += xr[k] * f16_to_f32(w16[(size_t)n * cols + k]);
+            for (int k = 0; k < k2; k++) acc += xr[cols + k] * f16_to_f32(w2[(size_t)n * k2 + k]);
+            const size_t o = (size_t)t * ldy + n;
+            switch (epi) {
+                case 0: y32[o] = (float)(acc + (double)beta * y32[o]); break;
+                case 1: y16[o] = f32_to_f16((float)acc); break;
+                case 2: y16[o] = f32_to_f16((float)(0.5 * acc * (1.0 + erf(acc * 0.70710678118654752440)))); break;
+                default: y32[o] = (float)((double)y32[o] + (gate ? (double)gate[n] : 1.0) * acc); break;
+            }
+        }
+        free(xr);
+    }
+}
+
+/*
  * Rotate-half RoPE (engine/src/kernels.cu:759-772, k_rope_half), in place on x [T, H*Dh]
  * (row stride ld elements), tables [T, Dh/2]:
  *   a = p[i], b = p[i+half];  p[i] = a*c - b*s;  p[i+half] = b*c + a*s

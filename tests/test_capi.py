@@ -78,6 +78,18 @@ def test_argument_validation_without_gpu(L):
     assert L.kiln_layernorm_mod16(p, p, None, p, 4, 2048, 1e-6, None) == kiln_amd.KILN_EINVAL
     assert L.kiln_add_gated(p, None, None, 4, 2048, None) == kiln_amd.KILN_EINVAL
     assert L.kiln_add_gated(p, p, None, -1, 2048, None) == kiln_amd.KILN_EINVAL
+    # linear16: the reference's eligibility (tcgemm16.cuh:177), epilogue code, alignment, output stride
+    q = ctypes.c_void_p(4096)
+    assert L.kiln_linear16(q, 128, q, 8, q, 128, 40, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_linear16(q, 128, q, 8, q, 96, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_linear16(q, 128, q, 8, q, 128, 64, 0, None, 0.0, q, q, 16, None) == kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_linear16(q, 128, q, 8, q, 128, 64, 4, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_linear16(q, 64, q, 8, q, 128, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_linear16(q, 128, ctypes.c_void_p(4104), 8, q, 128, 64, 0, None, 0.0, None, None, 0, None) == \
+        kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_linear16(q, 129, q, 8, q, 128, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_linear16(q, 128, None, 8, q, 128, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_linear16(None, 128, None, 0, None, 128, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_OK
     # more batch items than one launch takes
     assert L.kiln_dit_self_attn_fused(p, 1, 2048, p, p, p, 1, 2048, None, None, 1e-6, None, None, 5, 64, 16, None, 0,
                                       None) != kiln_amd.KILN_OK

@@ -250,3 +250,62 @@ def test_add_gated_cases():
     np.testing.assert_array_equal(oracle.add_gated(x, y, np.zeros(64, np.float32)), x)
     g = np.arange(64, dtype=np.float32) / 8
     np.testing.assert_allclose(oracle.add_gated(x, y, g), x + g[None, :] * y, rtol=0, atol=1e-6)
+
+
+def _f16(rng, shape, scale=1.0):
+    """Random fp16 bit patterns and their exact float64 values."""
+    v = (rng.standard_normal(shape) * scale).astype(np.float16)
+    return v.view(np.uint16), v.astype(np.float64)
+
+
+def test_linear16_matches_numpy_float64():
+    """oracle.linear16's product against numpy float64 matmul on the same fp16 values, every epilogue
+    (engine/src/kernels.cu:573-609, tcgemm16.cuh:145-175)."""
+    import math
+    rng = np.random.default_rng(21)
+    T, rows, cols = 37, 256, 96
+    xb, x = _f16(rng, (T, cols))
+    wb, w = _f16(rng, (rows, cols), cols ** -0.5)
+    acc = x @ w.T
+    y0 = rng.standard_normal((T, rows)).astype(np.float32)
+    got = oracle.linear16(xb, wb, oracle.EPI_F32)
+    np.testing.assert_allclose(got, acc, rtol=1e-6, atol=1e-6)
+    got = oracle.linear16(xb, wb, oracle.EPI_F32, y=y0, beta=0.5)
+    np.testing.assert_allclose(got, acc + 0.5 * y0, rtol=1e-6, atol=1e-6)
+    got = oracle.linear16(xb, wb, oracle.EPI_F16).view(np.float16).astype(np.float64)
+    np.testing.assert_array_equal(got, acc.astype(np.float32).astype(np.float16).astype(np.float64))
+    gelu = np.vectorize(lambda v: 0.5 * v * (1 + math.erf(v / math.sqrt(2))))(acc)
+    got = oracle.linear16(xb, wb, oracle.EPI_GELU16).view(np.float16).astype(np.float64)
+    np.testing.assert_array_equal(got, gelu.astype(np.float32).astype(np.float16).astype(np.float64))
+    g = rng.standard_normal(rows).astype(np.float32)
+    got = oracle.linear16(xb, wb, oracle.EPI_RESID, y=y0, gate=g)
+    np.testing.assert_allclose(got, y0 + g[None, :] * acc, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(oracle.linear16(xb, wb, oracle.EPI_RESID, y=y0), y0 + acc, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(oracle.linear16(xb, wb, oracle.EPI_RESID, y=y0, gate=np.zeros(rows, np.float32)), y0)
+
+
+def test_linear16_lora_is_concatenated_product():
+    """The folded second product equals one product over [x | a2] and [w | w2] (kernels.cu:564-566)."""
+    rng = np.random.default_rng(22)
+    T, rows, cols, k2 = 19, 128, 64, 32
+    xb, _ = _f16(rng, (T, cols))
+    wb, _ = _f16(rng, (rows, cols), 0.2)
+    ab, _ = _f16(rng, (T, k2))
+    vb, _ = _f16(rng, (rows, k2), 0.2)
+    got = oracle.linear16(xb, wb, oracle.EPI_F32, a2=ab, w2=vb)
+    ref = oracle.linear16(np.concatenate([xb, ab], 1), np.concatenate([wb, vb], 1), oracle.EPI_F32)
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_linear16_gelu_special_values():
+    """GELU(0) = 0, GELU(v) = v for large v, GELU(-v) = 0 for large v, GELU(1) = Phi(1) from its tabulated
+    value 0.8413447460685429."""
+    # one-column products: x = v, w = 1
+    vals = np.array([0.0, 1.0, 12.0, -12.0, 4.0], np.float16)
+    xb = vals.reshape(-1, 1).repeat(32, 1)
+    xb[:, 1:] = 0
+    wb = np.zeros((128, 32), np.float16)
+    wb[:, 0] = 1
+    got = oracle.linear16(xb.view(np.uint16), wb.view(np.uint16), oracle.EPI_GELU16).view(np.float16)[:, 0]
+    ref = np.array([0.0, 0.8413447460685429, 12.0, 0.0, 4.0 * 0.9999683287581669], np.float64)
+    np.testing.assert_array_equal(got, ref.astype(np.float16))

@@ -11,9 +11,10 @@
 // every product accumulates in fp32 (the MFMA's native accumulator): more accurate, same inputs.
 //
 // Design (gfx950, wave64):
-//  * workgroup tile 256 weight rows (n) x 256 activation rows (m), k tiles of 32; 8 waves in 2 (n) x 4 (m),
-//    each wave 128 n x 64 m = 8 x 4 blocks of v_mfma_f32_16x16x32_f16 (the shape that sustains the higher
-//    rate on a power-limited MI355X), 128 fp32 accumulators per lane, two waves per SIMD.
+//  * workgroup tile 256 weight rows (n) x 32*MB activation rows (m, MB = 8 or 7, whichever leaves the fewest
+//    idle CUs in the last round), k tiles of 32; 8 waves in 4 (n) x 2 (m), each wave 64 n x 16*MB m =
+//    4 x MB blocks of v_mfma_f32_16x16x32_f16 (the shape that sustains the higher rate on a power-limited
+//    MI355X), up to 128 fp32 accumulators per lane, two waves per SIMD.
 //  * the product is computed transposed, C^T = W A^T: the MFMA's A operand is a 16-row block of W, its B
 //    operand a 16-row block of A, and each lane ends with 4 consecutive output columns of one output row
 //    (one 16-byte fp32 / 8-byte fp16 store per block).
@@ -22,31 +23,49 @@
 //    chunks, chunk c of row r at position c ^ ((r >> 1) & 3): the DMA reads whole row segments (coalesced)
 //    and the MFMA operand reads (16 rows x one chunk per 16 lanes) are bank-conflict free.
 //  * the operands of k tile t+1 are read from LDS while the MFMAs of k tile t run.
-//  * each workgroup starts its k loop at its own offset (wrapping around): rows of one k tile are a 4 KB
-//    multiple apart, and an unstaggered grid would hit one L2 channel at a time.
 //  * 1-D grid, XCD-aware: workgroup b runs on XCD b % 8, and each XCD takes a contiguous range of tiles in
 //    groups of 4 row tiles, so the workgroups resident on one XCD share A and W tiles in its L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "internal.hpp"
 
 namespace kiln {
 
-namespace {
 
-constexpr int GBM = 256;             // activation rows (m) per workgroup
 constexpr int GBN = 256;             // weight rows (n) per workgroup
 constexpr int GBK = 32;              // k per tile: one 64-byte LDS row segment
 constexpr int GNS = 4;               // LDS ring stages
-constexpr int GTHR = 512;            // 8 waves
+constexpr int WAVES_N = 4;                   // waves along n; 2 along m
+constexpr int WAVES_M = 2;
+constexpr int NBW = GBN / 16 / WAVES_N;      // 16-row W blocks per wave
+constexpr int GTHR = 64 * WAVES_N * WAVES_M;
 constexpr int GROUP_M = 4;           // row tiles per raster group
-constexpr int REG_H = GBN * GBK;     // halves in one operand region of a stage (16 KB)
-constexpr int STAGE_H = 2 * REG_H;   // W region, then A region
-constexpr int DMA_PER_REG = REG_H * 2 / (GTHR * 16);  // 16-byte pieces per thread per region and k tile
+constexpr int W_REG_H = GBN * GBK;   // halves in the W region of a stage (16 KB)
+constexpr int W_DMA = W_REG_H * 2 / (GTHR * 16);  // 16-byte W pieces per thread per k tile
+
+// MB: 16-row activation blocks per wave; the workgroup's activation tile is 32*MB rows
+template <int MB>
+struct Tile {
+    static constexpr int BM = 32 * MB;
+    static constexpr int A_REG_H = BM * GBK;
+    static constexpr int STAGE_H = W_REG_H + A_REG_H;
+};
+// 16-byte A pieces per thread per k tile (the same for every tile height used, so that no array size in the
+// kernel depends on the template argument)
+constexpr int A_DMA = Tile<8>::A_REG_H * 2 / (GTHR * 16);
+constexpr int DMA_PER_TILE = W_DMA + A_DMA;
+static_assert(Tile<8>::A_REG_H * 2 == A_DMA * GTHR * 16 && Tile<7>::A_REG_H * 2 > (A_DMA - 1) * GTHR * 16, "A pieces");
 
 typedef __attribute__((address_space(3))) half8 lds_half8;
 typedef float f2v __attribute__((ext_vector_type(2)));
 
-#define GEMM_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (0xF << 8) | (((N) >> 4) << 14))
+// s_waitcnt vmcnt(N) (lgkmcnt and expcnt left alone). A device function, so that the host pass never checks
+// the builtin's constant argument inside the kernel template (where it depends on the tile height).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
 
 struct GemmParams {
     const _Float16* a;
@@ -65,15 +84,16 @@ struct GemmParams {
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-
 __device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.f + erff(v * 0.70710678118654752f)); }
 
-template <int EPI>
+template <int EPI, int MB>
 __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
-    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];  // GNS x 32 KB
+    using TL = Tile<MB>;
+    constexpr int BM = TL::BM, STAGE_H = TL::STAGE_H;
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];  // GNS stages of [W 256 rows | A BM rows]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wv >> 2, wm = wv & 3;
+    const int wn = wv / WAVES_M, wm = wv % WAVES_M;
 
     // tile of this workgroup: XCD b % 8 takes the contiguous range [xcd * per, (xcd + 1) * per)
     const int i = (int)(blockIdx.x & 7) * p.per + (int)(blockIdx.x >> 3);
@@ -82,71 +102,79 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
     const int g0 = (i / per_group) * GROUP_M;
     const int gsz = min(GROUP_M, p.tiles_m - g0);
     const int tm = g0 + (i % per_group) % gsz, tn = (i % per_group) / gsz;
-    const int m0 = tm * GBM, n0 = tn * GBN;
-    const int mrows = min(GBM, p.M - m0), nrows = min(GBN, p.N - n0);
+    const int m0 = tm * BM, n0 = tn * GBN;
+    const int mrows = min(BM, p.M - m0), nrows = min(GBN, p.N - n0);
 
     // DMA: this thread's 16-byte pieces q = tid + GTHR*r of a region: row q >> 2, LDS position q & 3 holding
-    // k chunk (q & 3) ^ ((row >> 1) & 3). Rows past the matrix re-read its last row (results unused). Per
-    // thread the byte offsets within the tile's rows are constants; the k tile goes in the scalar offset.
-    uint32_t voff_w[DMA_PER_REG], voff_a[DMA_PER_REG];
-    auto voffs = [&](int ld, uint32_t(&vw)[DMA_PER_REG], uint32_t(&va)[DMA_PER_REG]) {
+    // k chunk (q & 3) ^ ((row >> 1) & 3). Rows past the matrix re-read its last row (results unused); pieces
+    // past a region's end repeat the piece one round earlier (same source, same LDS bytes), so every wave
+    // issues the same number of DMA operations. The k tile goes in the scalar offset.
+    uint32_t voff_w[W_DMA], voff_a[A_DMA];
+    auto voffs = [&](int ld, uint32_t(&vw)[W_DMA], uint32_t(&va)[A_DMA]) {
 #pragma unroll
-        for (int r = 0; r < DMA_PER_REG; r++) {
+        for (int r = 0; r < W_DMA; r++) {
             const int q = tid + GTHR * r, row = q >> 2, c = (q & 3) ^ ((row >> 1) & 3);
             vw[r] = (uint32_t)(min(row, nrows - 1) * ld + c * 8) * 2;
+        }
+#pragma unroll
+        for (int r = 0; r < A_DMA; r++) {
+            int q = tid + GTHR * r;
+            if (q >= BM * 4) q -= GTHR;
+            const int row = q >> 2, c = (q & 3) ^ ((row >> 1) & 3);
             va[r] = (uint32_t)(min(row, mrows - 1) * ld + c * 8) * 2;
         }
     };
     voffs(p.K, voff_w, voff_a);
-    auto rsrc = [](const _Float16* base, size_t bytes) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(base), (short)0,
-                                                 (int)min(bytes, (size_t)0x7fffffff), 0x00020000 /* raw, CDNA */);
-    };
-    const __amdgpu_buffer_rsrc_t rw1 = rsrc(p.w + (size_t)n0 * p.K, (size_t)nrows * p.K * 2);
-    const __amdgpu_buffer_rsrc_t ra1 = rsrc(p.a + (size_t)m0 * p.K, (size_t)mrows * p.K * 2);
-    const __amdgpu_buffer_rsrc_t rw2 = rsrc(p.w2 + (size_t)n0 * p.K2, (size_t)nrows * p.K2 * 2);
-    const __amdgpu_buffer_rsrc_t ra2 = rsrc(p.a2 + (size_t)m0 * p.K2, (size_t)mrows * p.K2 * 2);
+#define GEMM_RSRC(base, bytes)                                                                             \
+    __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(base), (short)0, (int)min((size_t)(bytes), (size_t)0x7fffffff), \
+                                      0x00020000 /* raw, CDNA */)
+    const __amdgpu_buffer_rsrc_t rw1 = GEMM_RSRC(p.w + (size_t)n0 * p.K, (size_t)nrows * p.K * 2);
+    const __amdgpu_buffer_rsrc_t ra1 = GEMM_RSRC(p.a + (size_t)m0 * p.K, (size_t)mrows * p.K * 2);
+    const __amdgpu_buffer_rsrc_t rw2 = GEMM_RSRC(p.w2 + (size_t)n0 * p.K2, (size_t)nrows * p.K2 * 2);
+    const __amdgpu_buffer_rsrc_t ra2 = GEMM_RSRC(p.a2 + (size_t)m0 * p.K2, (size_t)mrows * p.K2 * 2);
     const int KT1 = p.K / GBK, KTT = KT1 + p.K2 / GBK;
-    // Staggered k order: rows of the same k tile sit one row stride apart (a multiple of 4 KB for the DiT's
-    // widths), so tiles at the same k of every workgroup would fall into the same L2 channel. Workgroup i
-    // starts its k loop (i % 16) x 256 bytes further along the row and wraps around.
-    const int kstag = ((i & 15) * 4) % KT1;
-
+    // the wave's 64 lanes write 1 KB of contiguous LDS at the wave-uniform base the DMA takes from M0
     auto dma = [&](int kt, int stage) {
-        _Float16* dw = lds + stage * STAGE_H + wv * 512;
-        _Float16* da = dw + REG_H;
-        if (kt < KT1) {
-            const int kk = kt + kstag < KT1 ? kt + kstag : kt + kstag - KT1;
-            const int so = kk * GBK * 2;
+        _Float16* base = lds + stage * STAGE_H;
+        _Float16* aq0[A_DMA];
 #pragma unroll
-            for (int r = 0; r < DMA_PER_REG; r++) {
+        for (int r = 0; r < A_DMA; r++) {
+            int q0 = GTHR * r + wv * 64;
+            if (q0 >= BM * 4) q0 -= GTHR;
+            aq0[r] = base + W_REG_H + q0 * 8;
+        }
+        if (kt < KT1) {
+            const int so = kt * GBK * 2;
+#pragma unroll
+            for (int r = 0; r < W_DMA; r++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rw1, (__attribute__((address_space(3))) void*)(dw + r * GTHR * 8), 16, voff_w[r], so, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    ra1, (__attribute__((address_space(3))) void*)(da + r * GTHR * 8), 16, voff_a[r], so, 0, 0);
-            }
+                    rw1, (__attribute__((address_space(3))) void*)(base + (GTHR * r + wv * 64) * 8), 16, voff_w[r], so, 0, 0);
+#pragma unroll
+            for (int r = 0; r < A_DMA; r++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra1, (__attribute__((address_space(3))) void*)aq0[r], 16,
+                                                         voff_a[r], so, 0, 0);
         } else {
             const int so = (kt - KT1) * GBK * 2;
-            uint32_t voff_w2[DMA_PER_REG], voff_a2[DMA_PER_REG];  // the LoRA tiles (few): offsets recomputed
-            voffs(p.K2, voff_w2, voff_a2);
+            uint32_t vw2[W_DMA], va2[A_DMA];  // the LoRA tiles (few): offsets recomputed
+            voffs(p.K2, vw2, va2);
 #pragma unroll
-            for (int r = 0; r < DMA_PER_REG; r++) {
+            for (int r = 0; r < W_DMA; r++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rw2, (__attribute__((address_space(3))) void*)(dw + r * GTHR * 8), 16, voff_w2[r], so, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    ra2, (__attribute__((address_space(3))) void*)(da + r * GTHR * 8), 16, voff_a2[r], so, 0, 0);
-            }
+                    rw2, (__attribute__((address_space(3))) void*)(base + (GTHR * r + wv * 64) * 8), 16, vw2[r], so, 0, 0);
+#pragma unroll
+            for (int r = 0; r < A_DMA; r++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra2, (__attribute__((address_space(3))) void*)aq0[r], 16,
+                                                         va2[r], so, 0, 0);
         }
     };
-    constexpr int DMA_PER_TILE = 2 * DMA_PER_REG;
 
     // operand reads: lane reads row (lane & 15) of a 16-row block, k chunk lane >> 4; blocks of one wave are
     // 1 KB apart, so they fold into ds_read_b128 immediate offsets.
     const uint32_t lds_base = (uint32_t)(size_t)(__attribute__((address_space(3))) _Float16*)lds;
     const int rl = lane & 15;
     const uint32_t swz = (uint32_t)((((lane >> 4) ^ ((rl >> 1) & 3))) * 16);
-    const uint32_t wbase = lds_base + (uint32_t)((wn * 128 + rl) * 64) + swz;
-    const uint32_t abase = lds_base + (uint32_t)(REG_H * 2 + (wm * 64 + rl) * 64) + swz;
+    const uint32_t wbase = lds_base + (uint32_t)((wn * NBW * 16 + rl) * 64) + swz;
+    const uint32_t abase = lds_base + (uint32_t)(W_REG_H * 2 + (wm * MB * 16 + rl) * 64) + swz;
     auto wfrag = [&](int stage, int nb) {
         return reinterpret_cast<const lds_half8*>((size_t)(wbase + stage * STAGE_H * 2))[nb * 64];
     };
@@ -154,67 +182,79 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
         return reinterpret_cast<const lds_half8*>((size_t)(abase + stage * STAGE_H * 2))[mb * 64];
     };
 
-    floatx4 acc[8][4];
+    floatx4 acc[NBW][MB];
 #pragma unroll
-    for (int nb = 0; nb < 8; nb++)
+    for (int nb = 0; nb < NBW; nb++)
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) acc[nb][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int mb = 0; mb < MB; mb++) acc[nb][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // prologue: k tiles 0..3 in flight; wait for tile 0 and read its operands
 #pragma unroll
     for (int s = 0; s < GNS; s++)
         if (s < KTT) dma(s, s);
-    if (KTT >= GNS) GEMM_WAIT_VMCNT((GNS - 1) * DMA_PER_TILE);
-    else GEMM_WAIT_VMCNT(0);
+    if (KTT >= GNS) wait_vmcnt<(GNS - 1) * DMA_PER_TILE>();
+    else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
-    // Operands in registers: the W blocks of the current k tile (each replaced by the next tile's block as soon
-    // as its four MFMAs are issued) and the A blocks of the current and the next tile (the loop alternates them).
-    half8 fw[8], fa[4], ga[4];
+    // Operands in registers: the activation blocks of the current k tile (each replaced by the next tile's
+    // block as soon as its four MFMAs are issued) and the W blocks of the current and the next tile (the loop
+    // alternates them).
+    half8 fa[MB], fw[NBW], gw[NBW];
 #pragma unroll
-    for (int b = 0; b < 8; b++) fw[b] = wfrag(0, b);
+    for (int b = 0; b < MB; b++) fa[b] = afrag(0, b);
 #pragma unroll
-    for (int b = 0; b < 4; b++) fa[b] = afrag(0, b);
+    for (int b = 0; b < NBW; b++) fw[b] = wfrag(0, b);
     __builtin_amdgcn_sched_barrier(0);
 
-    auto step = [&](int kt, half8(&ca)[4], half8(&na)[4]) {
+    // STEADY: kt + GNS < KTT (a refill to issue, the next tile's operands to read, GNS - 2 tiles in flight)
+    auto step = [&](auto steady_tag, int kt, half8(&cw)[NBW], half8(&nw)[NBW]) {
+        constexpr bool STEADY = decltype(steady_tag)::value;
         // tile kt+1 landed in every wave, and every wave has read tile kt's operands (stage kt is free):
-        // refill it with tile kt+4. Only tiles kt+2 and kt+3 may stay in flight.
+        // refill it with tile kt+GNS. Only tiles kt+2 .. kt+GNS-1 may stay in flight.
         const int ahead = KTT - 1 - kt;
-        if (ahead >= 3) GEMM_WAIT_VMCNT(2 * DMA_PER_TILE);
-        else if (ahead == 2) GEMM_WAIT_VMCNT(DMA_PER_TILE);
-        else GEMM_WAIT_VMCNT(0);
+        static_assert(GNS == 4, "the waits below assume a 4-stage ring");
+        if (STEADY || ahead >= 3) wait_vmcnt<2 * DMA_PER_TILE>();
+        else if (ahead == 3) wait_vmcnt<2 * DMA_PER_TILE>();
+        else if (ahead == 2) wait_vmcnt<DMA_PER_TILE>();
+        else wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage kt are complete
         __builtin_amdgcn_s_barrier();
-        if (kt + GNS < KTT) dma(kt + GNS, kt % GNS);
+        if (STEADY || kt + GNS < KTT) dma(kt + GNS, kt % GNS);
         __builtin_amdgcn_sched_barrier(0);
         const int nst = (kt + 1) % GNS;
-        if (ahead >= 1) {
+        const bool more = STEADY || ahead >= 1;
+        if (more) {
 #pragma unroll
-            for (int b = 0; b < 4; b++) na[b] = afrag(nst, b);
+            for (int b = 0; b < NBW; b++) nw[b] = wfrag(nst, b);
         }
 #pragma unroll
-        for (int nb = 0; nb < 8; nb++) {
+        for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) acc[nb][mb] = mfma16(fw[nb], ca[mb], acc[nb][mb]);
-            if (ahead >= 1) fw[nb] = wfrag(nst, nb);
+            for (int nb = 0; nb < NBW; nb++) acc[nb][mb] = mfma16(cw[nb], fa[mb], acc[nb][mb]);
+            if (more) fa[mb] = afrag(nst, mb);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
+    using True = std::true_type;
+    using False = std::false_type;
     int kt = 0;
-    for (; kt + 1 < KTT; kt += 2) {
-        step(kt, fa, ga);
-        step(kt + 1, ga, fa);
+    for (; kt + 1 + GNS < KTT; kt += 2) {
+        step(True{}, kt, fw, gw);
+        step(True{}, kt + 1, gw, fw);
     }
-    if (kt < KTT) step(kt, fa, ga);
+    for (; kt + 1 < KTT; kt += 2) {
+        step(False{}, kt, fw, gw);
+        step(False{}, kt + 1, gw, fw);
+    }
+    if (kt < KTT) step(False{}, kt, fw, gw);
 
-    // epilogue: lane holds rows m0 + wm*64 + mb*16 + (lane & 15), columns n0 + wn*128 + nb*16 + 4*(lane >> 4) + e
-    const int mrow = m0 + wm * 64 + rl;
-    const int ncol = n0 + wn * 128 + 4 * (lane >> 4);
-    if (ncol >= p.N) return;  // a 128-column half of the last tile past N (N % 256 == 128)
-    floatx4 gv[8];
+    // epilogue: lane holds rows m0 + wm*16*MB + mb*16 + (lane & 15), columns n0 + wn*64 + nb*16 + 4*(lane >> 4) + e
+    const int mrow = m0 + wm * 16 * MB + rl;
+    const int ncol = n0 + wn * NBW * 16 + 4 * (lane >> 4);
+    if (ncol >= p.N) return;  // a column range of the last tile past N (N % 256 == 128)
+    floatx4 gv[NBW];
     if constexpr (EPI == KILN_EPI_RESID) {
 #pragma unroll
-        for (int nb = 0; nb < 8; nb++) {
+        for (int nb = 0; nb < NBW; nb++) {
             if (p.gate) {
                 const float* g = p.gate + ncol + nb * 16;
                 gv[nb] = floatx4{g[0], g[1], g[2], g[3]};
@@ -224,11 +264,11 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
         }
     }
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++) {
+    for (int mb = 0; mb < MB; mb++) {
         const int m = mrow + mb * 16;
         if (m >= p.M) break;
 #pragma unroll
-        for (int nb = 0; nb < 8; nb++) {
+        for (int nb = 0; nb < NBW; nb++) {
             const int n = ncol + nb * 16;
             const size_t off = (size_t)m * p.ldc + n;
             const floatx4 v = acc[nb][mb];
@@ -276,7 +316,54 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
     }
 }
 
-}  // namespace
+static int cu_count() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus[dev] = 256;
+    return cus[dev];
+}
+
+template <int MB>
+static hipError_t launch_mb(GemmParams p, int epi, hipStream_t s) {
+    constexpr int BM = Tile<MB>::BM;
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + GBN - 1) / GBN;
+    p.total = p.tiles_m * p.tiles_n;
+    const int nb = (p.total + 7) / 8 * 8;
+    p.per = nb / 8;
+    const size_t lds = (size_t)GNS * Tile<MB>::STAGE_H * sizeof(_Float16);
+    void (*kern)(GemmParams) = nullptr;
+    switch (epi) {
+        case KILN_EPI_F32: kern = k_gemm16<KILN_EPI_F32, MB>; break;
+        case KILN_EPI_F16: kern = k_gemm16<KILN_EPI_F16, MB>; break;
+        case KILN_EPI_GELU16: kern = k_gemm16<KILN_EPI_GELU16, MB>; break;
+        case KILN_EPI_RESID: kern = k_gemm16<KILN_EPI_RESID, MB>; break;
+        default: return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(GTHR), lds, s, p);
+    return hipGetLastError();
+}
+
+
+// Activation tile height (32*MB rows, MB in {8, 7}): the one with the fewest CU rounds x rows per tile, one
+// workgroup per CU. M = 6912 (the DiT's CFG batch) is 27 tiles of 256 rows, so every grid of 256-row tiles
+// leaves 5/32 of the last round idle; 224-row tiles give 31 per column and fill 97%.
+int gemm16_mb(int M, int N) {
+    const int cus = cu_count(), tn = (N + GBN - 1) / GBN;
+    int best = 8;
+    long best_cost = -1;
+    for (int mb : {8, 7}) {
+        const long tiles = (long)((M + 32 * mb - 1) / (32 * mb)) * tn;
+        const long cost = (tiles + cus - 1) / cus * mb;
+        if (best_cost < 0 || cost < best_cost) {
+            best = mb;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
 
 hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s) {
     GemmParams p;
@@ -294,20 +381,8 @@ hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s) {
     p.beta = g.beta;
     const size_t esz = (g.epi == KILN_EPI_F32 || g.epi == KILN_EPI_RESID) ? 4 : 2;
     p.pairs = ((size_t)g.c % (4 * esz) != 0) || (g.ldc % 4 != 0);
-    p.tiles_m = (g.M + GBM - 1) / GBM;
-    p.tiles_n = (g.N + GBN - 1) / GBN;
-    p.total = p.tiles_m * p.tiles_n;
-    const int nb = (p.total + 7) / 8 * 8;
-    p.per = nb / 8;
-    const size_t lds = (size_t)GNS * STAGE_H * sizeof(_Float16);
-    switch (g.epi) {
-        case KILN_EPI_F32: hipLaunchKernelGGL(k_gemm16<KILN_EPI_F32>, dim3(nb), dim3(GTHR), lds, s, p); break;
-        case KILN_EPI_F16: hipLaunchKernelGGL(k_gemm16<KILN_EPI_F16>, dim3(nb), dim3(GTHR), lds, s, p); break;
-        case KILN_EPI_GELU16: hipLaunchKernelGGL(k_gemm16<KILN_EPI_GELU16>, dim3(nb), dim3(GTHR), lds, s, p); break;
-        case KILN_EPI_RESID: hipLaunchKernelGGL(k_gemm16<KILN_EPI_RESID>, dim3(nb), dim3(GTHR), lds, s, p); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if (gemm16_mb(g.M, g.N) == 7) return launch_mb<7>(p, g.epi, s);
+    return launch_mb<8>(p, g.epi, s);
 }
 
 }  // namespace kiln

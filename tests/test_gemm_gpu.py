@@ -174,3 +174,21 @@ def test_linear16_dit_shapes(gpu, epi, rows, cols):
         ref_o = ref_o.view(np.float16)
     _check(epi, y[idx.to(DEV)].float().cpu().double().numpy(), ref_o.astype(np.float64),
            _abs_acc(xs, w.cpu()), cols, gate.cpu().numpy() if gate is not None else None)
+
+
+@pytest.mark.parametrize("epi", [oracle.EPI_F32, oracle.EPI_GELU16])
+def test_linear16_tall_grid(gpu, epi):
+    """T = 8192, rows = 2048: 256-row tiles fill the 256 CUs exactly (the 224-row tiles of T = 6912 would
+    need a second round), so this grid takes the other tile height. 128 sampled rows against the oracle."""
+    T, rows, cols = 8192, 2048, 256
+    gen = torch.Generator().manual_seed(8)
+    x = _f16(gen, (T, cols))
+    w = _f16(gen, (rows, cols), cols ** -0.5)
+    dt = torch.float16 if epi == oracle.EPI_GELU16 else torch.float32
+    y = torch.zeros((T, rows), dtype=dt, device=DEV)
+    kiln_amd.linear16(y, x.to(DEV), w.to(DEV), epi=epi)
+    idx = torch.randperm(T, generator=gen)[:128]
+    ref = oracle.linear16(_bits(x[idx]), _bits(w), epi)
+    if epi == oracle.EPI_GELU16:
+        ref = ref.view(np.float16)
+    _check(epi, y[idx.to(DEV)].float().cpu().double().numpy(), ref.astype(np.float64), _abs_acc(x[idx], w), cols)

@@ -312,6 +312,34 @@ def main():
         f"{ag_tbps:.2f} TB/s")
     del x5, y5, n16
 
+    # the DiT block's linear layers (kiln_linear16, fused epilogues) at config 5's CFG batch, 2B model widths:
+    # Q/K/V and cross-Q (fp32 out), the two O projections (gated residual into x), MLP up (GELU, fp16 out)
+    # and MLP down (gated residual); torch's fp16 matmul (hipBLASLt, fp16 out, no epilogue) timed beside
+    g5 = torch.Generator(device=dev).manual_seed(55)
+    xs = torch.randn(R5, 8192, device=dev, generator=g5).half()
+    gate = torch.randn(8192, device=dev, generator=g5)
+    lin = {}
+    for name, N, K, epi in [("qkv", 2048, 2048, kiln_amd.KILN_EPI_F32), ("o_resid", 2048, 2048, kiln_amd.KILN_EPI_RESID),
+                            ("mlp_up_gelu", 8192, 2048, kiln_amd.KILN_EPI_GELU16),
+                            ("mlp_down_resid", 2048, 8192, kiln_amd.KILN_EPI_RESID)]:
+        a = xs[:, :K].contiguous()
+        w = (torch.randn(N, K, device=dev, generator=g5) * K ** -0.5).half()
+        fp16_out = epi == kiln_amd.KILN_EPI_GELU16
+        y = torch.zeros(R5, N, device=dev, dtype=torch.float16 if fp16_out else torch.float32)
+        g = gate[:N] if epi == kiln_amd.KILN_EPI_RESID else None
+        ms_l = tm.run(lambda: kiln_amd.linear16(y, a, w, epi=epi, gate=g), args.steps * 2, args.warmup)
+        ms_t = tm.run(lambda: torch.matmul(a, w.t()), args.steps * 2, args.warmup)
+        fl = 2.0 * R5 * N * K
+        lin[name] = dict(us=ms_l * 1e3, tflops=fl / ms_l / 1e9, torch_tflops=fl / ms_t / 1e9)
+        log(f"linear16 {name} ({R5} x {N} x {K}): {ms_l * 1e3:.1f} us {fl / ms_l / 1e9:.1f} TFLOP/s "
+            f"(torch fp16 matmul {fl / ms_t / 1e9:.1f})")
+        del w, y
+    del xs
+    # per DiT block: self Q, K, V and cross Q (4 x qkv), self and cross O (2 x o_resid), MLP up and down
+    blk_us = 4 * lin["qkv"]["us"] + 2 * lin["o_resid"]["us"] + lin["mlp_up_gelu"]["us"] + lin["mlp_down_resid"]["us"]
+    blk_fl = 2.0 * R5 * 2048 * 2048 * 6 + 2 * 2.0 * R5 * 8192 * 2048
+    log(f"linear16 per DiT block: {blk_us:.1f} us {blk_fl / blk_us / 1e6:.1f} TFLOP/s")
+
     traffic = None  # HBM bytes per launch of k_attn_fwd (config 4), from the committed rocprofv3 FETCH/WRITE runs
     tpath = os.path.join(ROOT, "profiles", "k_attn_fwd_config4_hbm_traffic.json")
     if os.path.exists(tpath):
@@ -359,6 +387,10 @@ def main():
             "layernorm_mod16_tbps": round(ln_tbps, 3),
             "add_gated_us": round(ms_ag * 1e3, 2),
             "add_gated_tbps": round(ag_tbps, 3),
+            "linear16_tflops": {k: round(v["tflops"], 1) for k, v in lin.items()},
+            "linear16_torch_f16out_tflops": {k: round(v["torch_tflops"], 1) for k, v in lin.items()},
+            "linear16_dit_block_us": round(blk_us, 1),
+            "linear16_dit_block_tflops": round(blk_fl / blk_us / 1e6, 1),
         },
         "roofline": {
             "bound": "mfma",

@@ -281,6 +281,11 @@ def linear16(y, x16, w16, epi=KILN_EPI_F32, gate=None, beta=0.0, a2=None, w2=Non
     T, cols = x16.shape
     rows = w16.shape[0]
     k2 = 0 if a2 is None else a2.shape[1]
+    for t in (x16, w16, a2, w2):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("linear16: x16, w16, a2 and w2 must be dense (contiguous) rows")
+    if y.stride(1) != 1:
+        raise ValueError("linear16: y rows must be contiguous")
     _check(lib().kiln_linear16(_ptr(y), y.stride(0), _ptr(x16), T, _ptr(w16), rows, cols, epi, _ptr(gate), beta,
                                _ptr(a2), _ptr(w2), k2, _stream(stream)))
     return y

@@ -114,6 +114,24 @@ typedef enum { KILN_EPI_F32 = 0, KILN_EPI_F16 = 1, KILN_EPI_GELU16 = 2, KILN_EPI
 int kiln_linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows, int cols, int epi,
                   const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2, kiln_stream_t stream);
 
+/* Bytes of the prepared form of a [rows, cols] linear16 weight: rows rounded up to 256, times cols, fp16. */
+size_t kiln_linear16_prepped_weight_bytes(int rows, int cols);
+
+/* Replaces weight_to_f16() for a linear16 weight (engine/src/kernels.cu:531-544, called at load,
+ * engine/src/dit.cu:100): converts W [rows, cols] (fp16, or bf16 when src_bf16 != 0: clamped to +-65504 and
+ * rounded to nearest even, as k_bf16_to_f16) into the prepared tile layout that kiln_linear16_prepped streams
+ * with one contiguous 16 KB read per 256-row x 32-k tile. wp: kiln_linear16_prepped_weight_bytes(rows, cols)
+ * bytes, 16-byte aligned, not overlapping w. Same eligibility as kiln_linear16. */
+int kiln_linear16_prepare_weight(uint16_t* wp, const uint16_t* w, int rows, int cols, int src_bf16,
+                                 kiln_stream_t stream);
+
+/* kiln_linear16 with the weight in the prepared layout (wp from kiln_linear16_prepare_weight of the same rows
+ * and cols). The LoRA product's w2 stays in plain [rows, k2] rows. Results equal kiln_linear16's on the
+ * fp16 weight. */
+int kiln_linear16_prepped(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* wp, int rows, int cols,
+                          int epi, const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2,
+                          kiln_stream_t stream);
+
 /* Host-side Cosmos 3D RoPE tables for an Hp x Wp patch grid (engine/src/dit.cu:196-215):
  * cos_t, sin_t are HOST arrays of Hp*Wp*64 floats. */
 int kiln_cosmos_rope_tables(float* cos_t, float* sin_t, int Hp, int Wp);

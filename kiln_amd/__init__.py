@@ -37,6 +37,9 @@ _SIGS = {
     "kiln_layernorm_mod16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "kiln_add_gated": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "kiln_linear16": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
+    "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
+    "kiln_linear16_prepped_weight_bytes": (_sz, [_i, _i]),
+    "kiln_linear16_prepare_weight": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "kiln_nag_combine": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _f, _f, _f, _vp]),
     "kiln_cosmos_rope_tables": (_i, [_vp, _vp, _i, _i]),
     "kiln_kv_prepped_bytes": (_sz, [_i, _i]),
@@ -273,10 +276,35 @@ def cross_attn_nag(out, q, B, T, H, kvps, Lks, npads, q_norm_w=None, eps=1e-6, k
     return out
 
 
+def linear16_prepare_weight(w, stream=None):
+    """weight_to_f16 for a linear16 weight (engine/src/kernels.cu:531-544) into the prepared layout.
+
+    w: fp16 or bf16 [rows, cols] (contiguous). Returns a PreppedWeight for linear16(..., w16=<it>)."""
+    import torch
+    if not w.is_contiguous():
+        raise ValueError("linear16_prepare_weight: w must be contiguous")
+    rows, cols = w.shape
+    nbytes = lib().kiln_linear16_prepped_weight_bytes(rows, cols)
+    buf = torch.empty(max(nbytes, 2) // 2, dtype=torch.float16, device=w.device)
+    _check(lib().kiln_linear16_prepare_weight(_ptr(buf), _ptr(w), rows, cols, int(w.dtype == torch.bfloat16),
+                                              _stream(stream)))
+    return PreppedWeight(buf, rows, cols)
+
+
+class PreppedWeight:
+    """A linear16 weight in the prepared tile layout (kiln_linear16_prepare_weight)."""
+
+    def __init__(self, buf, rows, cols):
+        self.buf, self.shape = buf, (rows, cols)
+
+    def is_contiguous(self):
+        return True
+
+
 def linear16(y, x16, w16, epi=KILN_EPI_F32, gate=None, beta=0.0, a2=None, w2=None, stream=None):
     """linear16() (engine/src/kernels.cu:573-609): acc = x16 w16^T (+ a2 w2^T) with epilogue `epi`.
 
-    x16 fp16 [T, cols], w16 fp16 [rows, cols], y [T, >= rows] (fp32 for F32/RESID, fp16 for F16/GELU16,
+    x16 fp16 [T, cols], w16 fp16 [rows, cols] or a PreppedWeight, y [T, >= rows] (fp32 for F32/RESID, fp16 for F16/GELU16,
     row stride y.stride(0)); a2 [T, k2] / w2 [rows, k2] fp16 or None."""
     T, cols = x16.shape
     rows = w16.shape[0]
@@ -286,6 +314,10 @@ def linear16(y, x16, w16, epi=KILN_EPI_F32, gate=None, beta=0.0, a2=None, w2=Non
             raise ValueError("linear16: x16, w16, a2 and w2 must be dense (contiguous) rows")
     if y.stride(1) != 1:
         raise ValueError("linear16: y rows must be contiguous")
-    _check(lib().kiln_linear16(_ptr(y), y.stride(0), _ptr(x16), T, _ptr(w16), rows, cols, epi, _ptr(gate), beta,
-                               _ptr(a2), _ptr(w2), k2, _stream(stream)))
+    if isinstance(w16, PreppedWeight):
+        fn, wptr = lib().kiln_linear16_prepped, _ptr(w16.buf)
+    else:
+        fn, wptr = lib().kiln_linear16, _ptr(w16)
+    _check(fn(_ptr(y), y.stride(0), _ptr(x16), T, wptr, rows, cols, epi, _ptr(gate), beta, _ptr(a2), _ptr(w2), k2,
+              _stream(stream)))
     return y

@@ -421,21 +421,22 @@ int kiln_add_gated(float* x, const float* y, const float* gate, int rows, int di
     return hip_check(kiln::launch_add_gated(x, y, gate, rows, dim, (hipStream_t)stream), "add_gated launch");
 }
 
-int kiln_linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows, int cols, int epi,
-                  const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2, kiln_stream_t stream) {
-    if (epi < KILN_EPI_F32 || epi > KILN_EPI_RESID) return fail(KILN_EINVAL, "linear16: epilogue %d", epi);
+static int linear16_impl(const char* fn, void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows,
+                         int cols, int epi, const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2,
+                         bool wprep, kiln_stream_t stream) {
+    if (epi < KILN_EPI_F32 || epi > KILN_EPI_RESID) return fail(KILN_EINVAL, "%s: epilogue %d", fn, epi);
     if (T < 0 || rows <= 0 || cols <= 0 || k2 < 0)
-        return fail(KILN_EINVAL, "linear16: bad sizes T=%d rows=%d cols=%d k2=%d", T, rows, cols, k2);
+        return fail(KILN_EINVAL, "%s: bad sizes T=%d rows=%d cols=%d k2=%d", fn, T, rows, cols, k2);
     if (rows % 128 || cols % 32 || k2 % 32)
-        return fail(KILN_EUNSUPPORTED, "linear16: needs rows %% 128 == 0, cols %% 32 == 0, k2 %% 32 == 0 (rows=%d cols=%d k2=%d)",
-                    rows, cols, k2);
-    if (ldy < rows) return fail(KILN_EINVAL, "linear16: ldy=%d < rows=%d", ldy, rows);
+        return fail(KILN_EUNSUPPORTED, "%s: needs rows %% 128 == 0, cols %% 32 == 0, k2 %% 32 == 0 (rows=%d cols=%d k2=%d)",
+                    fn, rows, cols, k2);
+    if (ldy < rows) return fail(KILN_EINVAL, "%s: ldy=%d < rows=%d", fn, ldy, rows);
     if (T == 0) return KILN_OK;
-    if (!y || !x16 || !w16 || (k2 && (!a2 || !w2))) return fail(KILN_EINVAL, "linear16: null pointer");
+    if (!y || !x16 || !w16 || (k2 && (!a2 || !w2))) return fail(KILN_EINVAL, "%s: null pointer", fn);
     if (!aligned16(x16) || !aligned16(w16) || (k2 && (!aligned16(a2) || !aligned16(w2))))
-        return fail(KILN_EUNSUPPORTED, "linear16: operands must be 16-byte aligned");
+        return fail(KILN_EUNSUPPORTED, "%s: operands must be 16-byte aligned", fn);
     const size_t esz = (epi == KILN_EPI_F32 || epi == KILN_EPI_RESID) ? 4 : 2;
-    if (ldy % 2 || (size_t)y % (2 * esz)) return fail(KILN_EUNSUPPORTED, "linear16: y rows must hold element pairs");
+    if (ldy % 2 || (size_t)y % (2 * esz)) return fail(KILN_EUNSUPPORTED, "%s: y rows must hold element pairs", fn);
     kiln::GemmLaunch g;
     g.a = x16;
     g.w = w16;
@@ -450,7 +451,39 @@ int kiln_linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* 
     g.M = T;
     g.N = rows;
     g.epi = epi;
+    g.wprep = wprep;
     return hip_check(kiln::launch_gemm16(g, (hipStream_t)stream), "linear16 launch");
+}
+
+int kiln_linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows, int cols, int epi,
+                  const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2, kiln_stream_t stream) {
+    return linear16_impl("linear16", y, ldy, x16, T, w16, rows, cols, epi, gate, beta, a2, w2, k2, false, stream);
+}
+
+int kiln_linear16_prepped(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* wp, int rows, int cols,
+                          int epi, const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2,
+                          kiln_stream_t stream) {
+    return linear16_impl("linear16_prepped", y, ldy, x16, T, wp, rows, cols, epi, gate, beta, a2, w2, k2, true, stream);
+}
+
+size_t kiln_linear16_prepped_weight_bytes(int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    return kiln::gemm16_prepped_bytes(rows, cols);
+}
+
+int kiln_linear16_prepare_weight(uint16_t* wp, const uint16_t* w, int rows, int cols, int src_bf16,
+                                 kiln_stream_t stream) {
+    if (rows <= 0 || cols <= 0) return fail(KILN_EINVAL, "linear16_prepare_weight: bad sizes rows=%d cols=%d", rows, cols);
+    if (rows % 128 || cols % 32)
+        return fail(KILN_EUNSUPPORTED, "linear16_prepare_weight: needs rows %% 128 == 0, cols %% 32 == 0 (rows=%d cols=%d)",
+                    rows, cols);
+    if (!wp || !w) return fail(KILN_EINVAL, "linear16_prepare_weight: null pointer");
+    if (!aligned16(wp) || !aligned16(w)) return fail(KILN_EUNSUPPORTED, "linear16_prepare_weight: 16-byte alignment");
+    const size_t nb = kiln::gemm16_prepped_bytes(rows, cols);
+    if ((const char*)wp < (const char*)w + (size_t)rows * cols * 2 && (const char*)w < (const char*)wp + nb)
+        return fail(KILN_EINVAL, "linear16_prepare_weight: wp overlaps w");
+    return hip_check(kiln::launch_gemm_wprep(wp, w, rows, cols, src_bf16 != 0, (hipStream_t)stream),
+                     "linear16_prepare_weight launch");
 }
 
 int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {

@@ -79,6 +79,7 @@ struct GemmParams {
     float beta;
     int tiles_m, tiles_n, total, per;
     int pairs;  // output rows or base not 16-byte (fp32) / 8-byte (fp16) aligned: store element pairs
+    int wprep;  // w is in the prepared tile layout (kiln_linear16_prepare_weight), not [N, K] rows
 };
 
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
@@ -110,11 +111,12 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
     // past a region's end repeat the piece one round earlier (same source, same LDS bytes), so every wave
     // issues the same number of DMA operations. The k tile goes in the scalar offset.
     uint32_t voff_w[W_DMA], voff_a[A_DMA];
-    auto voffs = [&](int ld, uint32_t(&vw)[W_DMA], uint32_t(&va)[A_DMA]) {
+    auto voffs = [&](int ld, bool prep, uint32_t(&vw)[W_DMA], uint32_t(&va)[A_DMA]) {
 #pragma unroll
         for (int r = 0; r < W_DMA; r++) {
             const int q = tid + GTHR * r, row = q >> 2, c = (q & 3) ^ ((row >> 1) & 3);
-            vw[r] = (uint32_t)(min(row, nrows - 1) * ld + c * 8) * 2;
+            // prepared W (main product only): the k tile's 16 KB block is already in LDS order
+            vw[r] = prep ? (uint32_t)q * 16 : (uint32_t)(min(row, nrows - 1) * ld + c * 8) * 2;
         }
 #pragma unroll
         for (int r = 0; r < A_DMA; r++) {
@@ -124,11 +126,13 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
             va[r] = (uint32_t)(min(row, mrows - 1) * ld + c * 8) * 2;
         }
     };
-    voffs(p.K, voff_w, voff_a);
+    voffs(p.K, p.wprep != 0, voff_w, voff_a);
 #define GEMM_RSRC(base, bytes)                                                                             \
     __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(base), (short)0, (int)min((size_t)(bytes), (size_t)0x7fffffff), \
                                       0x00020000 /* raw, CDNA */)
-    const __amdgpu_buffer_rsrc_t rw1 = GEMM_RSRC(p.w + (size_t)n0 * p.K, (size_t)nrows * p.K * 2);
+    const __amdgpu_buffer_rsrc_t rw1 =
+        p.wprep ? GEMM_RSRC(p.w + (size_t)tn * GBN * p.K, (size_t)GBN * p.K * 2)
+                : GEMM_RSRC(p.w + (size_t)n0 * p.K, (size_t)nrows * p.K * 2);
     const __amdgpu_buffer_rsrc_t ra1 = GEMM_RSRC(p.a + (size_t)m0 * p.K, (size_t)mrows * p.K * 2);
     const __amdgpu_buffer_rsrc_t rw2 = GEMM_RSRC(p.w2 + (size_t)n0 * p.K2, (size_t)nrows * p.K2 * 2);
     const __amdgpu_buffer_rsrc_t ra2 = GEMM_RSRC(p.a2 + (size_t)m0 * p.K2, (size_t)mrows * p.K2 * 2);
@@ -145,10 +149,11 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
         }
         if (kt < KT1) {
             const int so = kt * GBK * 2;
+            const int sow = p.wprep ? kt * W_REG_H * 2 : so;
 #pragma unroll
             for (int r = 0; r < W_DMA; r++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rw1, (__attribute__((address_space(3))) void*)(base + (GTHR * r + wv * 64) * 8), 16, voff_w[r], so, 0, 0);
+                    rw1, (__attribute__((address_space(3))) void*)(base + (GTHR * r + wv * 64) * 8), 16, voff_w[r], sow, 0, 0);
 #pragma unroll
             for (int r = 0; r < A_DMA; r++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra1, (__attribute__((address_space(3))) void*)aq0[r], 16,
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
         } else {
             const int so = (kt - KT1) * GBK * 2;
             uint32_t vw2[W_DMA], va2[A_DMA];  // the LoRA tiles (few): offsets recomputed
-            voffs(p.K2, vw2, va2);
+            voffs(p.K2, false, vw2, va2);
 #pragma unroll
             for (int r = 0; r < W_DMA; r++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -316,6 +321,47 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
     }
 }
 
+// Prepared weight layout: [ceil(N/256) column tiles][K/32 k tiles][16 KB block], the block holding the 256 rows
+// x 32 k of the tile in the kernel's LDS order (16-byte piece q: row q >> 2, k chunk (q & 3) ^ ((row >> 1) & 3));
+// rows past N are zero. The k loop's W DMA then reads one contiguous 16 KB block per k tile instead of 256 row
+// segments 2 KB or more apart (measured 14-17% faster on the DiT shapes). The source is fp16 or bf16; bf16 is
+// clamped to the fp16 range and rounded to nearest even (the reference's weight_to_f16, kernels.cu:531-544).
+__global__ void k_gemm_wprep(_Float16* __restrict__ wp, const uint16_t* __restrict__ w, int N, int K, int src_bf16,
+                             long total) {
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int q = (int)(g & 1023);
+    const long blk = g >> 10;
+    const int KT = K / GBK;
+    const int kt = (int)(blk % KT), tn = (int)(blk / KT);
+    const int row = q >> 2, c = (q & 3) ^ ((row >> 1) & 3);
+    const int n = tn * GBN + row;
+    half8 v = {};
+    if (n < N) {
+        const uint16_t* src = w + (size_t)n * K + kt * GBK + c * 8;
+        if (src_bf16) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint16_t b = (uint16_t)(raw[e / 2] >> (16 * (e & 1)));
+                v[e] = (_Float16)fminf(fmaxf(bf16_to_f32(b), -65504.f), 65504.f);
+            }
+        } else {
+            v = *reinterpret_cast<const half8*>(src);
+        }
+    }
+    *reinterpret_cast<half8*>(wp + g * 8) = v;
+}
+
+size_t gemm16_prepped_bytes(int N, int K) { return (size_t)((N + GBN - 1) / GBN) * GBN * K * sizeof(_Float16); }
+
+hipError_t launch_gemm_wprep(uint16_t* wp, const uint16_t* w, int N, int K, bool src_bf16, hipStream_t s) {
+    const long total = (long)((N + GBN - 1) / GBN) * (K / GBK) * 1024;
+    hipLaunchKernelGGL(k_gemm_wprep, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<_Float16*>(wp), w, N, K, src_bf16 ? 1 : 0, total);
+    return hipGetLastError();
+}
+
 static int cu_count() {
     static int cus[64] = {};
     int dev = 0;
@@ -381,6 +427,7 @@ hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s) {
     p.beta = g.beta;
     const size_t esz = (g.epi == KILN_EPI_F32 || g.epi == KILN_EPI_RESID) ? 4 : 2;
     p.pairs = ((size_t)g.c % (4 * esz) != 0) || (g.ldc % 4 != 0);
+    p.wprep = g.wprep ? 1 : 0;
     if (gemm16_mb(g.M, g.N) == 7) return launch_mb<7>(p, g.epi, s);
     return launch_mb<8>(p, g.epi, s);
 }

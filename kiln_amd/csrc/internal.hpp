@@ -68,8 +68,12 @@ struct GemmLaunch {
     float beta;
     int M, N;
     int epi;
+    bool wprep;  // w in the prepared layout of launch_gemm_wprep
 };
 hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s);
+// Weight [N, K] (fp16, or bf16 converted as the reference's weight_to_f16) into the prepared tile layout.
+size_t gemm16_prepped_bytes(int N, int K);
+hipError_t launch_gemm_wprep(uint16_t* wp, const uint16_t* w, int N, int K, bool src_bf16, hipStream_t s);
 
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s);

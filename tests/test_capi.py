@@ -90,6 +90,13 @@ def test_argument_validation_without_gpu(L):
     assert L.kiln_linear16(q, 129, q, 8, q, 128, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EUNSUPPORTED
     assert L.kiln_linear16(q, 128, None, 8, q, 128, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EINVAL
     assert L.kiln_linear16(None, 128, None, 0, None, 128, 64, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_OK
+    # prepared weights: size, eligibility, overlap
+    assert L.kiln_linear16_prepped_weight_bytes(384, 64) == 512 * 64 * 2
+    assert L.kiln_linear16_prepped_weight_bytes(0, 64) == 0
+    assert L.kiln_linear16_prepare_weight(q, q, 96, 64, 0, None) == kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_linear16_prepare_weight(q, ctypes.c_void_p(4096 + 1024), 128, 64, 0, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_linear16_prepare_weight(None, q, 128, 64, 0, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_linear16_prepped(q, 128, q, 8, q, 128, 40, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EUNSUPPORTED
     # more batch items than one launch takes
     assert L.kiln_dit_self_attn_fused(p, 1, 2048, p, p, p, 1, 2048, None, None, 1e-6, None, None, 5, 64, 16, None, 0,
                                       None) != kiln_amd.KILN_OK

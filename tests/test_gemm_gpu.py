@@ -192,3 +192,42 @@ def test_linear16_tall_grid(gpu, epi):
     if epi == oracle.EPI_GELU16:
         ref = ref.view(np.float16)
     _check(epi, y[idx.to(DEV)].float().cpu().double().numpy(), ref.astype(np.float64), _abs_acc(x[idx], w), cols)
+
+
+@pytest.mark.parametrize("T,rows,cols,k2", [(37, 256, 96, 0), (300, 384, 1024, 0), (129, 256, 512, 64), (8192, 2048, 256, 0)])
+def test_linear16_prepped_weight_bit_identical(gpu, T, rows, cols, k2):
+    """kiln_linear16_prepped on the prepared weight gives bit-identical outputs to kiln_linear16 on the fp16
+    weight, every epilogue (the same products in the same order; only the weight's memory layout differs)."""
+    gen = torch.Generator().manual_seed(9)
+    x = _f16(gen, (T, cols)).to(DEV)
+    w = _f16(gen, (rows, cols), cols ** -0.5).to(DEV)
+    a2 = _f16(gen, (T, k2)).to(DEV) if k2 else None
+    w2 = _f16(gen, (rows, k2), 0.1).to(DEV) if k2 else None
+    wp = kiln_amd.linear16_prepare_weight(w)
+    gate = torch.randn(rows, generator=gen).to(DEV)
+    for epi in EPIS:
+        dt = torch.float16 if epi in (oracle.EPI_F16, oracle.EPI_GELU16) else torch.float32
+        y0 = torch.randn((T, rows), generator=gen).to(DEV).to(dt)
+        ya, yb = y0.clone(), y0.clone()
+        g = gate if epi == oracle.EPI_RESID else None
+        kiln_amd.linear16(ya, x, w, epi=epi, gate=g, beta=0.25 if epi == oracle.EPI_F32 else 0.0, a2=a2, w2=w2)
+        kiln_amd.linear16(yb, x, wp, epi=epi, gate=g, beta=0.25 if epi == oracle.EPI_F32 else 0.0, a2=a2, w2=w2)
+        torch.cuda.synchronize()
+        assert torch.equal(ya.view(torch.int16 if dt == torch.float16 else torch.int32),
+                           yb.view(torch.int16 if dt == torch.float16 else torch.int32)), f"epi {epi}"
+
+
+def test_linear16_prepare_weight_from_bf16(gpu):
+    """bf16 weights are clamped to the fp16 range and rounded to nearest even (the reference's k_bf16_to_f16,
+    engine/src/kernels.cu:531-536), then used as the fp16 weight: equal to the oracle on the converted values."""
+    T, rows, cols = 64, 128, 64
+    gen = torch.Generator().manual_seed(10)
+    x = _f16(gen, (T, cols))
+    wb = (torch.randn((rows, cols), generator=gen) * 0.3).to(torch.bfloat16)
+    wb[0, :4] = torch.tensor([70000.0, -1e6, 65504.0, 1.0009765625], dtype=torch.bfloat16)  # clamp and rounding
+    w16 = wb.float().clamp(-65504, 65504).to(torch.float16)
+    wp = kiln_amd.linear16_prepare_weight(wb.to(DEV))
+    y = torch.zeros((T, rows), device=DEV)
+    kiln_amd.linear16(y, x.to(DEV), wp)
+    ref = oracle.linear16(_bits(x), _bits(w16), oracle.EPI_F32)
+    _check(oracle.EPI_F32, y.cpu().double().numpy(), ref.astype(np.float64), _abs_acc(x, w16), cols)

@@ -327,13 +327,16 @@ def main():
         fp16_out = epi == kiln_amd.KILN_EPI_GELU16
         y = torch.zeros(R5, N, device=dev, dtype=torch.float16 if fp16_out else torch.float32)
         g = gate[:N] if epi == kiln_amd.KILN_EPI_RESID else None
-        ms_l = tm.run(lambda: kiln_amd.linear16(y, a, w, epi=epi, gate=g), args.steps * 2, args.warmup)
+        wp = kiln_amd.linear16_prepare_weight(w)  # weights are prepared once, at load
+        ms_l = tm.run(lambda: kiln_amd.linear16(y, a, wp, epi=epi, gate=g), args.steps * 2, args.warmup)
+        ms_p = tm.run(lambda: kiln_amd.linear16(y, a, w, epi=epi, gate=g), args.steps * 2, args.warmup)
         ms_t = tm.run(lambda: torch.matmul(a, w.t()), args.steps * 2, args.warmup)
         fl = 2.0 * R5 * N * K
-        lin[name] = dict(us=ms_l * 1e3, tflops=fl / ms_l / 1e9, torch_tflops=fl / ms_t / 1e9)
-        log(f"linear16 {name} ({R5} x {N} x {K}): {ms_l * 1e3:.1f} us {fl / ms_l / 1e9:.1f} TFLOP/s "
-            f"(torch fp16 matmul {fl / ms_t / 1e9:.1f})")
-        del w, y
+        lin[name] = dict(us=ms_l * 1e3, tflops=fl / ms_l / 1e9, plain_tflops=fl / ms_p / 1e9,
+                         torch_tflops=fl / ms_t / 1e9)
+        log(f"linear16 {name} ({R5} x {N} x {K}): {ms_l * 1e3:.1f} us {fl / ms_l / 1e9:.1f} TFLOP/s prepared weight, "
+            f"{fl / ms_p / 1e9:.1f} plain (torch fp16 matmul {fl / ms_t / 1e9:.1f})")
+        del w, wp, y
     del xs
     # per DiT block: self Q, K, V and cross Q (4 x qkv), self and cross O (2 x o_resid), MLP up and down
     blk_us = 4 * lin["qkv"]["us"] + 2 * lin["o_resid"]["us"] + lin["mlp_up_gelu"]["us"] + lin["mlp_down_resid"]["us"]
@@ -388,6 +391,7 @@ def main():
             "add_gated_us": round(ms_ag * 1e3, 2),
             "add_gated_tbps": round(ag_tbps, 3),
             "linear16_tflops": {k: round(v["tflops"], 1) for k, v in lin.items()},
+            "linear16_plain_weight_tflops": {k: round(v["plain_tflops"], 1) for k, v in lin.items()},
             "linear16_torch_f16out_tflops": {k: round(v["torch_tflops"], 1) for k, v in lin.items()},
             "linear16_dit_block_us": round(blk_us, 1),
             "linear16_dit_block_tflops": round(blk_fl / blk_us / 1e6, 1),

@@ -145,6 +145,42 @@ def dit_step_case(torch, kiln_amd, dev, nblocks=28, Hp=48, Wp=72, B=2, L=512, se
     return dict(T=T, step=step, flop=flop)
 
 
+def linear16_cases(torch, kiln_amd, tm, dev, steps, warmup):
+    """The DiT block's linear layers (kiln_linear16, fused epilogues) at config 5's CFG batch (2 x 3456 rows),
+    2B model widths: Q/K/V and cross-Q (fp32 out), the two O projections (gated residual into x), MLP up (GELU,
+    fp16 out) and MLP down (gated residual); torch's fp16 matmul (hipBLASLt, fp16 out, no epilogue) beside."""
+    R5 = 2 * 3456
+    g5 = torch.Generator(device=dev).manual_seed(55)
+    xs = torch.randn(R5, 8192, device=dev, generator=g5).half()
+    gate = torch.randn(8192, device=dev, generator=g5)
+    lin = {}
+    for name, N, K, epi in [("qkv", 2048, 2048, kiln_amd.KILN_EPI_F32), ("o_resid", 2048, 2048, kiln_amd.KILN_EPI_RESID),
+                            ("mlp_up_gelu", 8192, 2048, kiln_amd.KILN_EPI_GELU16),
+                            ("mlp_down_resid", 2048, 8192, kiln_amd.KILN_EPI_RESID)]:
+        a = xs[:, :K].contiguous()
+        w = (torch.randn(N, K, device=dev, generator=g5) * K ** -0.5).half()
+        fp16_out = epi == kiln_amd.KILN_EPI_GELU16
+        y = torch.zeros(R5, N, device=dev, dtype=torch.float16 if fp16_out else torch.float32)
+        g = gate[:N] if epi == kiln_amd.KILN_EPI_RESID else None
+        wp = kiln_amd.linear16_prepare_weight(w)  # weights are prepared once, at load
+        ms_l = tm.run(lambda: kiln_amd.linear16(y, a, wp, epi=epi, gate=g), steps * 2, warmup)
+        ms_p = tm.run(lambda: kiln_amd.linear16(y, a, w, epi=epi, gate=g), steps * 2, warmup)
+        ms_t = tm.run(lambda: torch.matmul(a, w.t()), steps * 2, warmup)
+        fl = 2.0 * R5 * N * K
+        lin[name] = dict(us=ms_l * 1e3, tflops=fl / ms_l / 1e9, plain_tflops=fl / ms_p / 1e9,
+                         torch_tflops=fl / ms_t / 1e9)
+        log(f"linear16 {name} ({R5} x {N} x {K}): {ms_l * 1e3:.1f} us {fl / ms_l / 1e9:.1f} TFLOP/s prepared weight, "
+            f"{fl / ms_p / 1e9:.1f} plain (torch fp16 matmul {fl / ms_t / 1e9:.1f})")
+        del w, wp, y
+    del xs
+    # per DiT block: self Q, K, V and cross Q (4 x qkv), self and cross O (2 x o_resid), MLP up and down
+    blk_us = 4 * lin["qkv"]["us"] + 2 * lin["o_resid"]["us"] + lin["mlp_up_gelu"]["us"] + lin["mlp_down_resid"]["us"]
+    blk_fl = 2.0 * R5 * 2048 * 2048 * 6 + 2 * 2.0 * R5 * 8192 * 2048
+    log(f"linear16 per DiT block: {blk_us:.1f} us {blk_fl / blk_us / 1e6:.1f} TFLOP/s")
+
+    return lin, blk_us, blk_fl
+
+
 def run_probe():
     """Runs kiln_amd/probe/mfma_mix (built by kiln_amd/build.py) in a child process; {} if it is not built."""
     import subprocess
@@ -203,6 +239,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--main-only", action="store_true",
                     help="run only the config-4 attention kernel loop (for rocprofv3 runs)")
+    ap.add_argument("--linear16-only", action="store_true",
+                    help="run only the DiT-shape linear16 cases (for rocprofv3 runs)")
     ap.add_argument("--probe", action="store_true",
                     help="only run the sustained matrix-core probe (kiln_amd/probe/mfma_mix) and print its JSON")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
@@ -234,6 +272,10 @@ def main():
         dst = torch.empty_like(src)
         ms = tm.run(lambda: dst.copy_(src), args.steps, args.warmup)
         log(f"copy {args.copy_cal} MiB: {ms * 1e3:.1f} us  {2 * src.numel() * 4 / ms / 1e6:.1f} GB/s")
+        return 0
+
+    if args.linear16_only:
+        linear16_cases(torch, kiln_amd, tm, dev, args.steps, args.warmup)
         return 0
 
     cfg4 = self_attn_case(torch, kiln_amd, 64, 64, 2, 4, dev)
@@ -312,36 +354,7 @@ def main():
         f"{ag_tbps:.2f} TB/s")
     del x5, y5, n16
 
-    # the DiT block's linear layers (kiln_linear16, fused epilogues) at config 5's CFG batch, 2B model widths:
-    # Q/K/V and cross-Q (fp32 out), the two O projections (gated residual into x), MLP up (GELU, fp16 out)
-    # and MLP down (gated residual); torch's fp16 matmul (hipBLASLt, fp16 out, no epilogue) timed beside
-    g5 = torch.Generator(device=dev).manual_seed(55)
-    xs = torch.randn(R5, 8192, device=dev, generator=g5).half()
-    gate = torch.randn(8192, device=dev, generator=g5)
-    lin = {}
-    for name, N, K, epi in [("qkv", 2048, 2048, kiln_amd.KILN_EPI_F32), ("o_resid", 2048, 2048, kiln_amd.KILN_EPI_RESID),
-                            ("mlp_up_gelu", 8192, 2048, kiln_amd.KILN_EPI_GELU16),
-                            ("mlp_down_resid", 2048, 8192, kiln_amd.KILN_EPI_RESID)]:
-        a = xs[:, :K].contiguous()
-        w = (torch.randn(N, K, device=dev, generator=g5) * K ** -0.5).half()
-        fp16_out = epi == kiln_amd.KILN_EPI_GELU16
-        y = torch.zeros(R5, N, device=dev, dtype=torch.float16 if fp16_out else torch.float32)
-        g = gate[:N] if epi == kiln_amd.KILN_EPI_RESID else None
-        wp = kiln_amd.linear16_prepare_weight(w)  # weights are prepared once, at load
-        ms_l = tm.run(lambda: kiln_amd.linear16(y, a, wp, epi=epi, gate=g), args.steps * 2, args.warmup)
-        ms_p = tm.run(lambda: kiln_amd.linear16(y, a, w, epi=epi, gate=g), args.steps * 2, args.warmup)
-        ms_t = tm.run(lambda: torch.matmul(a, w.t()), args.steps * 2, args.warmup)
-        fl = 2.0 * R5 * N * K
-        lin[name] = dict(us=ms_l * 1e3, tflops=fl / ms_l / 1e9, plain_tflops=fl / ms_p / 1e9,
-                         torch_tflops=fl / ms_t / 1e9)
-        log(f"linear16 {name} ({R5} x {N} x {K}): {ms_l * 1e3:.1f} us {fl / ms_l / 1e9:.1f} TFLOP/s prepared weight, "
-            f"{fl / ms_p / 1e9:.1f} plain (torch fp16 matmul {fl / ms_t / 1e9:.1f})")
-        del w, wp, y
-    del xs
-    # per DiT block: self Q, K, V and cross Q (4 x qkv), self and cross O (2 x o_resid), MLP up and down
-    blk_us = 4 * lin["qkv"]["us"] + 2 * lin["o_resid"]["us"] + lin["mlp_up_gelu"]["us"] + lin["mlp_down_resid"]["us"]
-    blk_fl = 2.0 * R5 * 2048 * 2048 * 6 + 2 * 2.0 * R5 * 8192 * 2048
-    log(f"linear16 per DiT block: {blk_us:.1f} us {blk_fl / blk_us / 1e6:.1f} TFLOP/s")
+    lin, blk_us, blk_fl = linear16_cases(torch, kiln_amd, tm, dev, args.steps, args.warmup)
 
     traffic = None  # HBM bytes per launch of k_attn_fwd (config 4), from the committed rocprofv3 FETCH/WRITE runs
     tpath = os.path.join(ROOT, "profiles", "k_attn_fwd_config4_hbm_traffic.json")

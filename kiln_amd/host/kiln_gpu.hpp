@@ -76,6 +76,51 @@ inline void add_gated(float* x, const float* y, const float* gate, int rows, int
     check(kiln_add_gated(x, y, gate, rows, dim, (kiln_stream_t)stream_ref()), "add_gated");
 }
 
+// ---- linear16 (engine/src/gpu.h:125-127, kernels.cu:573-609): fp16 GEMM with fused epilogue ----
+
+enum class Epi16 { F32 = KILN_EPI_F32, F16 = KILN_EPI_F16, Gelu16 = KILN_EPI_GELU16, Resid = KILN_EPI_RESID };
+
+// A linear16 weight converted at load (the reference's weight_to_f16, kernels.cu:531-544) into the prepared
+// layout; owns its device buffer. src: [rows, cols] fp16, or bf16 when src_bf16.
+class Linear16Weight {
+   public:
+    Linear16Weight(const uint16_t* src, int rows, int cols, bool src_bf16) : rows_(rows), cols_(cols) {
+        const size_t n = kiln_linear16_prepped_weight_bytes(rows, cols);
+        if (!n || hipMalloc(&p_, n) != hipSuccess) throw std::runtime_error("kiln: linear16 weight allocation failed");
+        check(kiln_linear16_prepare_weight(p_, src, rows, cols, src_bf16 ? 1 : 0, (kiln_stream_t)stream_ref()),
+              "linear16_prepare_weight");
+    }
+    ~Linear16Weight() {
+        if (p_) (void)hipFree(p_);
+    }
+    Linear16Weight(const Linear16Weight&) = delete;
+    Linear16Weight& operator=(const Linear16Weight&) = delete;
+    const uint16_t* data() const { return p_; }
+    int rows() const { return rows_; }
+    int cols() const { return cols_; }
+
+   private:
+    uint16_t* p_ = nullptr;
+    int rows_, cols_;
+};
+
+// y [T, ldy] (fp32 for F32/Resid, fp16 for F16/Gelu16) from x16 [T, W.cols()] (dense fp16 rows). The folded
+// LoRA product (kernels.cu:564-600) comes in as a2 [T, k2] and w2 [W.rows(), k2] (fp16, k2 % 32 == 0).
+inline void linear16(void* y, int ldy, const uint16_t* x16, int T, const Linear16Weight& W, Epi16 epi,
+                     const float* gate = nullptr, float beta = 0.f, const uint16_t* a2 = nullptr,
+                     const uint16_t* w2 = nullptr, int k2 = 0) {
+    check(kiln_linear16_prepped(y, ldy, x16, T, W.data(), W.rows(), W.cols(), (int)epi, gate, beta, a2, w2, k2,
+                                (kiln_stream_t)stream_ref()),
+          "linear16");
+}
+// The same on a plain fp16 weight [rows, cols].
+inline void linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows, int cols, Epi16 epi,
+                     const float* gate = nullptr, float beta = 0.f) {
+    check(kiln_linear16(y, ldy, x16, T, w16, rows, cols, (int)epi, gate, beta, nullptr, nullptr, 0,
+                        (kiln_stream_t)stream_ref()),
+          "linear16");
+}
+
 // NAG combine of fp16 rows (the k_nag<__half> launch of the fp16-activation forward).
 inline void nag16(uint16_t* a, const uint16_t* an, int T, int dim, float scale, float tau, float alpha) {
     check(kiln_nag_combine(a, dim, an, dim, KILN_F16, T, dim, scale, tau, alpha, (kiln_stream_t)stream_ref()),

@@ -4,6 +4,8 @@
 // rows real, unconditional 64 of 64, NAG negative 33 of 64), self-attention with QK-RMSNorm + Cosmos RoPE, and
 // cross-attention with NAG on item 0. A host reference in double precision restates the same steps
 // (kernels.cu:656-666 RMSNorm, 759-772 RoPE, 809-826 attention with npad zero keys, dit.cu:295-324 NAG).
+// Then the block's linear layers: a bf16 weight prepared at load (kiln::Linear16Weight, weight_to_f16) and
+// linear16 with the GELU16 and gated-residual epilogues (kernels.cu:573-609) against a double restatement.
 // Exit status 1 if any output leaves max-abs 2e-3 / mean-abs 2e-4.
 #include <hip/hip_runtime.h>
 
@@ -225,6 +227,60 @@ int main() {
             ok &= compare(what, out, o, (size_t)b * T * LD);
         }
         for (void* p : {(void*)dq, (void*)dk, (void*)dv, (void*)dqn, (void*)dkn, (void*)dqc, (void*)dqcn}) CK(hipFree(p));
+    }
+    // ---- the block's linear layers through kiln::Linear16Weight (prepared at load from bf16) ----
+    {
+        const int R = B * T, IN = LD, OUT = 2 * LD;
+        std::vector<uint16_t> xh((size_t)R * IN), wb((size_t)OUT * IN);
+        std::vector<double> xd(xh.size()), wd(wb.size());
+        for (size_t i = 0; i < xh.size(); i++) {
+            const _Float16 h = (_Float16)nd(rng);
+            std::memcpy(&xh[i], &h, 2);
+            xd[i] = (double)h;
+        }
+        for (size_t i = 0; i < wb.size(); i++) {
+            const float f = nd(rng) * 0.05f;
+            uint32_t u;
+            std::memcpy(&u, &f, 4);
+            wb[i] = (uint16_t)(u >> 16);
+            wd[i] = (double)(_Float16)bf16f(wb[i]);  // bf16 -> fp16 (round to nearest even), as weight_to_f16
+        }
+        std::vector<float> gate(OUT), res((size_t)R * OUT);
+        for (auto& g : gate) g = nd(rng);
+        for (auto& r : res) r = nd(rng);
+        uint16_t *dx = to_dev(xh), *dwb = to_dev(wb), *dh;
+        float *dg = to_dev(gate), *dr = to_dev(res);
+        CK(hipMalloc(&dh, (size_t)R * OUT * 2));
+        kiln::Linear16Weight W(dwb, OUT, IN, true);
+        kiln::linear16(dh, OUT, dx, R, W, kiln::Epi16::Gelu16);
+        kiln::linear16(dr, OUT, dx, R, W, kiln::Epi16::Resid, dg);
+        std::vector<uint16_t> gh((size_t)R * OUT);
+        std::vector<float> rr((size_t)R * OUT);
+        CK(hipMemcpy(gh.data(), dh, gh.size() * 2, hipMemcpyDeviceToHost));
+        CK(hipMemcpy(rr.data(), dr, rr.size() * 4, hipMemcpyDeviceToHost));
+        double emg = 0, emr = 0;
+        bool lok = true;
+        for (int r = 0; r < R; r++)
+            for (int n = 0; n < OUT; n++) {
+                double acc = 0, aabs = 0;
+                for (int k = 0; k < IN; k++) {
+                    acc += xd[(size_t)r * IN + k] * wd[(size_t)n * IN + k];
+                    aabs += std::fabs(xd[(size_t)r * IN + k] * wd[(size_t)n * IN + k]);
+                }
+                const double bar = std::sqrt((double)IN) * std::ldexp(1.0, -21) * aabs + 1e-7;
+                const double gl = 0.5 * acc * (1.0 + std::erf(acc / std::sqrt(2.0)));
+                const double eg = std::fabs((double)h2f(gh[(size_t)r * OUT + n]) - gl);
+                const double ulp = std::ldexp(1.0, (int)std::floor(std::log2(std::max(std::fabs(gl), 6.1e-5))) - 10);
+                const double rf = (double)res[(size_t)r * OUT + n] + (double)gate[n] * acc;
+                const double er = std::fabs((double)rr[(size_t)r * OUT + n] - rf);
+                lok &= eg <= bar + ulp && er <= bar * std::fabs(gate[n]) + std::fabs(rf) * std::ldexp(1.0, -23);
+                emg = std::max(emg, eg);
+                emr = std::max(emr, er);
+            }
+        printf("%-40s max-abs %.3e (GELU16) %.3e (RESID)  %s\n", "linear16 (prepared bf16 weight)", emg, emr,
+               lok ? "ok" : "FAIL");
+        ok &= lok;
+        for (void* p : {(void*)dx, (void*)dwb, (void*)dh, (void*)dg, (void*)dr}) CK(hipFree(p));
     }
     printf("%s\n", ok ? "dit_section_test: all ok" : "dit_section_test: FAILED");
     return ok ? 0 : 1;

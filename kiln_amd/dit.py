@@ -1,0 +1,93 @@
+"""One Cosmos-Predict2 DiT block on the fp16-activation path, composed from the library's entry points.
+
+Mirrors the block loop of the reference's Dit::forward_batch for G.fp16 && G.tc16 (engine/src/dit.cu:455-494):
+
+    N16 = layernorm_mod16(X; shift, scale of the self-attention modulation)
+    Q, K, V = linear16(N16, sa_q / sa_k / sa_v)                         fp32 (one launch on [Wq; Wk; Wv])
+    A16 = attention16(rmsnorm+rope(Q), rmsnorm+rope(K), V) per item      kiln_dit_self_attn_fused, one launch
+    X += gate * linear16(A16, sa_o)                                      RESID epilogue
+    N16 = layernorm_mod16(X; cross-attention modulation)
+    Q = linear16(N16, ca_q)                                              fp32
+    A16 = attention16(rmsnorm(Q), context K/V of each item) (+ NAG on item 0)   kiln_cross_attn_nag
+    X += gate * linear16(A16, ca_o)
+    N16 = layernorm_mod16(X; MLP modulation)
+    H16 = GELU(linear16(N16, mlp1))                                      GELU16 epilogue
+    X += gate * linear16(H16, mlp2)
+
+The modulation vector of a block is [9 * D] fp32: (shift, scale, gate) for self-attention, cross-attention
+and the MLP (engine/src/dit.cu:266-268, used at :460-493). Context K/V are prepared once per generation and
+block (Dit::cache_context, engine/src/dit.cu:217-234): K = rmsnorm(ctx @ ca_k^T; ca_kn), V = ctx @ ca_v^T.
+Every call below goes to the HIP library; there is no CPU path.
+"""
+import torch
+
+from . import (KILN_EPI_F32, KILN_EPI_GELU16, KILN_EPI_RESID, cross_attn_nag, dit_self_attn,
+               dit_self_attn_workspace_bytes, kv_prepare, layernorm_mod, linear16, linear16_prepare_weight)
+
+HD = 128
+
+
+class Block16:
+    """The weights of one DiT block in the layout the fp16 path consumes: every linear16 weight prepared at
+    load (kiln_linear16_prepare_weight; Q/K/V stacked into one [3D, D] weight), norm weights bf16 [128]."""
+
+    def __init__(self, sa_qkv, sa_o, ca_q, ca_o, mlp1, mlp2, sa_qn, sa_kn, ca_qn, ca_kn, ca_k=None, ca_v=None):
+        self.sa_qkv = linear16_prepare_weight(sa_qkv)
+        self.sa_o = linear16_prepare_weight(sa_o)
+        self.ca_q = linear16_prepare_weight(ca_q)
+        self.ca_o = linear16_prepare_weight(ca_o)
+        self.mlp1 = linear16_prepare_weight(mlp1)
+        self.mlp2 = linear16_prepare_weight(mlp2)
+        self.sa_qn, self.sa_kn, self.ca_qn, self.ca_kn = sa_qn, sa_kn, ca_qn, ca_kn
+        self.ca_k, self.ca_v = ca_k, ca_v  # fp32 [D, Dctx] context projections (used by prepare_context)
+        self.D = sa_o.shape[0]
+        self.F = mlp1.shape[0]
+
+    def prepare_context(self, ctx, eps=1e-6):
+        """Dit::cache_context for this block (engine/src/dit.cu:217-234): the real rows of a context
+        [L, Dctx] fp32 -> prepared K/V (K RMS-normed with ca_kn)."""
+        k = ctx @ self.ca_k.t()
+        v = ctx @ self.ca_v.t()
+        return kv_prepare(k, v, self.D // HD, k_norm_w=self.ca_kn, eps=eps)
+
+
+class Workspace:
+    """Activation buffers of one forward at B items x T tokens (the reference's arena slices N, big, A)."""
+
+    def __init__(self, B, T, D, F, device):
+        R = B * T
+        self.n16 = torch.empty(R, D, dtype=torch.float16, device=device)
+        self.qkv = torch.empty(R, 3 * D, dtype=torch.float32, device=device)
+        self.a16 = torch.empty(R, D, dtype=torch.float16, device=device)
+        self.an16 = torch.empty(T, D, dtype=torch.float16, device=device)
+        self.h16 = torch.empty(R, F, dtype=torch.float16, device=device)
+        self.attn_ws = torch.empty(dit_self_attn_workspace_bytes(B, T, D // HD), dtype=torch.uint8, device=device)
+
+
+def block_forward16(X, mods, blk, ws, B, T, rope, ctx, nag=None, eps=1e-6):
+    """X [B*T, D] fp32 (updated in place) through one block. mods [9*D] fp32; rope = (cos, sin) [T, 64];
+    ctx: per item (prepared K/V, real rows, padding rows); nag: None or (prepared K/V, real, padding, scale,
+    tau, alpha) for item 0."""
+    D, H = blk.D, blk.D // HD
+    mo, mc, mm = mods[0:3 * D], mods[3 * D:6 * D], mods[6 * D:9 * D]
+    q, k, v = ws.qkv[:, 0:D], ws.qkv[:, D:2 * D], ws.qkv[:, 2 * D:3 * D]
+    # self-attention
+    layernorm_mod(ws.n16, X, mo[D:2 * D], mo[0:D], eps)
+    linear16(ws.qkv, ws.n16, blk.sa_qkv, epi=KILN_EPI_F32)
+    dit_self_attn(ws.a16, q, k, v, B, T, H, blk.sa_qn, blk.sa_kn, rope, eps=eps, workspace=ws.attn_ws)
+    linear16(X, ws.a16, blk.sa_o, epi=KILN_EPI_RESID, gate=mo[2 * D:3 * D])
+    # cross-attention, each item against its own context (+ NAG on item 0)
+    layernorm_mod(ws.n16, X, mc[D:2 * D], mc[0:D], eps)
+    linear16(q, ws.n16, blk.ca_q, epi=KILN_EPI_F32)
+    kvps = [c[0] for c in ctx[:B]]
+    args = dict(q_norm_w=blk.ca_qn, eps=eps)
+    if nag is not None:
+        args.update(kvp_neg=nag[0], Lk_neg=nag[1], npad_neg=nag[2], out_neg=ws.an16, scale=nag[3], tau=nag[4],
+                    alpha=nag[5])
+    cross_attn_nag(ws.a16, q, B, T, H, kvps, [c[1] for c in ctx[:B]], [c[2] for c in ctx[:B]], **args)
+    linear16(X, ws.a16, blk.ca_o, epi=KILN_EPI_RESID, gate=mc[2 * D:3 * D])
+    # MLP
+    layernorm_mod(ws.n16, X, mm[D:2 * D], mm[0:D], eps)
+    linear16(ws.h16, ws.n16, blk.mlp1, epi=KILN_EPI_GELU16)
+    linear16(X, ws.h16, blk.mlp2, epi=KILN_EPI_RESID, gate=mm[2 * D:3 * D])
+    return X

@@ -132,6 +132,30 @@ int kiln_linear16_prepped(void* y, int ldy, const uint16_t* x16, int T, const ui
                           int epi, const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2,
                           kiln_stream_t stream);
 
+/* ---- the DiT forward's passes around the transformer blocks (engine/src/dit.cu:242-272, 414-417, 537-545) ---- */
+
+/* Replaces matvec() (engine/src/gpu.h:122, kernels.cu k_matvec): y[r] = sum_c W[r][c] x[c] (+ add[r]), W bf16
+ * [rows, cols] row-major, x fp32 [cols], add fp32 [rows] or NULL. The per-step modulation vectors. */
+int kiln_matvec_bf16(float* y, const uint16_t* w_bf16, const float* x, const float* add, int rows, int cols,
+                     kiln_stream_t stream);
+/* Replaces silu() (engine/src/gpu.h:142, kernels.cu:735-739): y = x / (1 + exp(-x)), n elements, in place
+ * allowed. */
+int kiln_silu(float* y, const float* x, size_t n, kiln_stream_t stream);
+/* Replaces k_patchify (engine/src/dit.cu:174-182): a 16-channel latent [16, Hl, Wl] (Hl, Wl even) into
+ * tokens [T = Hl/2 * Wl/2, 68], feature 4c + 2m + n = channel c of pixel (2ty + m, 2tx + n); features 64-67
+ * (the padding-mask channel) are 0. */
+int kiln_patchify(float* tok, const float* latent, int Hl, int Wl, kiln_stream_t stream);
+/* Replaces k_unpatchify (engine/src/dit.cu:184-191): tokens [T, 64] (row stride ldt) into the latent
+ * [16, Hl, Wl], feature 32 p1 + 16 p2 + c -> channel c of pixel (2ty + p1, 2tx + p2). */
+int kiln_unpatchify(float* latent, const float* tok, int ldt, int Hl, int Wl, kiln_stream_t stream);
+/* Replaces linear() for the DiT's small fp32 layers (engine/src/gpu.h:118, kernels.cu:508-529; the x embedder
+ * and the final layer, dit.cu:417,542): y [T, rows] (row stride ldy) = x [T, cols] (row stride ldx) W^T with
+ * W bf16 [rows, cols], fp32 arithmetic. */
+int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* w_bf16, int T, int rows, int cols,
+                    kiln_stream_t stream);
+/* Replaces cfg_combine() (engine/src/gpu.h:144, kernels.cu:1058-1062): v = vn + cfg * (v - vn), n elements. */
+int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream_t stream);
+
 /* Host-side Cosmos 3D RoPE tables for an Hp x Wp patch grid (engine/src/dit.cu:196-215):
  * cos_t, sin_t are HOST arrays of Hp*Wp*64 floats. */
 int kiln_cosmos_rope_tables(float* cos_t, float* sin_t, int Hp, int Wp);

@@ -37,6 +37,12 @@ _SIGS = {
     "kiln_layernorm_mod16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "kiln_add_gated": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "kiln_linear16": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
+    "kiln_matvec_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "kiln_silu": (_i, [_vp, _vp, _sz, _vp]),
+    "kiln_patchify": (_i, [_vp, _vp, _i, _i, _vp]),
+    "kiln_unpatchify": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "kiln_linear_f32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
+    "kiln_cfg_combine": (_i, [_vp, _vp, _f, _sz, _vp]),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "kiln_linear16_prepped_weight_bytes": (_sz, [_i, _i]),
     "kiln_linear16_prepare_weight": (_i, [_vp, _vp, _i, _i, _i, _vp]),
@@ -321,3 +327,42 @@ def linear16(y, x16, w16, epi=KILN_EPI_F32, gate=None, beta=0.0, a2=None, w2=Non
     _check(fn(_ptr(y), y.stride(0), _ptr(x16), T, wptr, rows, cols, epi, _ptr(gate), beta, _ptr(a2), _ptr(w2), k2,
               _stream(stream)))
     return y
+
+
+def matvec(y, w_bf16, x, add=None, stream=None):
+    """matvec (engine/src/gpu.h:122): y = W x (+ add), W bf16 [rows, cols]."""
+    _check(lib().kiln_matvec_bf16(_ptr(y), _ptr(w_bf16), _ptr(x), _ptr(add), w_bf16.shape[0], w_bf16.shape[1],
+                                  _stream(stream)))
+    return y
+
+
+def silu(y, x, stream=None):
+    """silu (engine/src/kernels.cu:735-739), elementwise over x.numel()."""
+    _check(lib().kiln_silu(_ptr(y), _ptr(x), x.numel(), _stream(stream)))
+    return y
+
+
+def patchify(tok, latent, stream=None):
+    """k_patchify (engine/src/dit.cu:174-182): latent [16, Hl, Wl] -> tok [T, 68]."""
+    _check(lib().kiln_patchify(_ptr(tok), _ptr(latent), latent.shape[1], latent.shape[2], _stream(stream)))
+    return tok
+
+
+def unpatchify(latent, tok, stream=None):
+    """k_unpatchify (engine/src/dit.cu:184-191): tok [T, >= 64] (row stride tok.stride(0)) -> latent [16, Hl, Wl]."""
+    _check(lib().kiln_unpatchify(_ptr(latent), _ptr(tok), tok.stride(0), latent.shape[1], latent.shape[2],
+                                 _stream(stream)))
+    return latent
+
+
+def linear_f32(y, x, w_bf16, stream=None):
+    """linear (engine/src/kernels.cu:508-529) for small fp32 layers: y [T, rows] = x [T, cols] W^T, W bf16."""
+    _check(lib().kiln_linear_f32(_ptr(y), y.stride(0), _ptr(x), x.stride(0), _ptr(w_bf16), x.shape[0],
+                                 w_bf16.shape[0], w_bf16.shape[1], _stream(stream)))
+    return y
+
+
+def cfg_combine(v, vn, cfg, stream=None):
+    """cfg_combine (engine/src/kernels.cu:1058-1062): v = vn + cfg (v - vn)."""
+    _check(lib().kiln_cfg_combine(_ptr(v), _ptr(vn), cfg, v.numel(), _stream(stream)))
+    return v

@@ -486,6 +486,49 @@ int kiln_linear16_prepare_weight(uint16_t* wp, const uint16_t* w, int rows, int 
                      "linear16_prepare_weight launch");
 }
 
+int kiln_matvec_bf16(float* y, const uint16_t* w_bf16, const float* x, const float* add, int rows, int cols,
+                     kiln_stream_t stream) {
+    if (rows < 0 || cols <= 0) return fail(KILN_EINVAL, "matvec: bad sizes rows=%d cols=%d", rows, cols);
+    if (rows && (!y || !w_bf16 || !x)) return fail(KILN_EINVAL, "matvec: null pointer");
+    if (!rows) return KILN_OK;
+    return hip_check(kiln::launch_matvec_bf16(y, w_bf16, x, add, rows, cols, (hipStream_t)stream), "matvec launch");
+}
+
+int kiln_silu(float* y, const float* x, size_t n, kiln_stream_t stream) {
+    if (n && (!y || !x)) return fail(KILN_EINVAL, "silu: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_silu(y, x, n, (hipStream_t)stream), "silu launch");
+}
+
+int kiln_patchify(float* tok, const float* latent, int Hl, int Wl, kiln_stream_t stream) {
+    if (Hl <= 0 || Wl <= 0 || Hl % 2 || Wl % 2) return fail(KILN_EINVAL, "patchify: Hl=%d Wl=%d (even, > 0)", Hl, Wl);
+    if (!tok || !latent) return fail(KILN_EINVAL, "patchify: null pointer");
+    return hip_check(kiln::launch_patchify(tok, latent, Hl, Wl, (hipStream_t)stream), "patchify launch");
+}
+
+int kiln_unpatchify(float* latent, const float* tok, int ldt, int Hl, int Wl, kiln_stream_t stream) {
+    if (Hl <= 0 || Wl <= 0 || Hl % 2 || Wl % 2 || ldt < 64)
+        return fail(KILN_EINVAL, "unpatchify: Hl=%d Wl=%d ldt=%d", Hl, Wl, ldt);
+    if (!tok || !latent) return fail(KILN_EINVAL, "unpatchify: null pointer");
+    return hip_check(kiln::launch_unpatchify(latent, tok, ldt, Hl, Wl, (hipStream_t)stream), "unpatchify launch");
+}
+
+int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* w_bf16, int T, int rows, int cols,
+                    kiln_stream_t stream) {
+    if (T < 0 || rows <= 0 || cols <= 0 || ldy < rows || ldx < cols)
+        return fail(KILN_EINVAL, "linear_f32: bad sizes T=%d rows=%d cols=%d ldy=%d ldx=%d", T, rows, cols, ldy, ldx);
+    if (!T) return KILN_OK;
+    if (!y || !x || !w_bf16) return fail(KILN_EINVAL, "linear_f32: null pointer");
+    return hip_check(kiln::launch_linear_f32(y, ldy, x, ldx, w_bf16, T, rows, cols, (hipStream_t)stream),
+                     "linear_f32 launch");
+}
+
+int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream_t stream) {
+    if (n && (!v || !vn)) return fail(KILN_EINVAL, "cfg_combine: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_cfg_combine(v, vn, cfg, n, (hipStream_t)stream), "cfg_combine launch");
+}
+
 int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {
     if (T < 0 || H <= 0 || Dh <= 0 || Dh % 2) return fail(KILN_EINVAL, "bad sizes");
     if (T && (!x || !cos_t || !sin_t)) return fail(KILN_EINVAL, "null pointer");

@@ -1,0 +1,152 @@
+// The DiT forward's small passes around the transformer blocks (gfx950): per-step modulation matvecs with bf16
+// weights, SiLU, patch embedding layout (patchify / unpatchify), the fp32 linear layers with bf16 weights
+// (x embedder, final layer) and the CFG combine. Each is HBM- or launch-bound; none is on the attention path.
+//
+// Contracts (the reference's, engine/src/kernels.cu and engine/src/dit.cu):
+//   matvec       y[r] = sum_c W[r][c] x[c] (+ add[r]), W bf16 [rows, cols]        kernels.cu k_matvec
+//   silu         y = v / (1 + exp(-v))                                               kernels.cu:735-739
+//   patchify     tok [T, 68] from a 16-channel latent [16, Hl, Wl], 2x2 patches      dit.cu:174-182
+//   unpatchify   latent [16, Hl, Wl] from tok [T, 64]                                dit.cu:184-191
+//   linear_f32   y [T, rows] = x [T, cols] W^T, W bf16 [rows, cols], fp32 math      kernels.cu:508-529 (linear)
+//   cfg_combine  v = vn + cfg (v - vn)                                              kernels.cu:1058-1062
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace kiln {
+
+// One wave per row: 16-byte bf16 loads striding the row, fp32 partial sums, a wave reduction.
+__global__ __launch_bounds__(256) void k_matvec_bf16(float* __restrict__ y, const uint16_t* __restrict__ W,
+                                                     const float* __restrict__ x, const float* __restrict__ add,
+                                                     int rows, int cols) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const uint16_t* w = W + (size_t)row * cols;
+    float s = 0.f;
+    if ((cols & 7) == 0 && ((size_t)w & 15) == 0 && ((size_t)x & 15) == 0) {
+        for (int c = lane * 8; c < cols; c += 64 * 8) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(w + c);
+            const floatx4 xa = *reinterpret_cast<const floatx4*>(x + c);
+            const floatx4 xb = *reinterpret_cast<const floatx4*>(x + c + 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                s += __uint_as_float(raw[e] << 16) * (e < 2 ? xa[2 * e] : xb[2 * e - 4]);
+                s += __uint_as_float(raw[e] & 0xffff0000u) * (e < 2 ? xa[2 * e + 1] : xb[2 * e - 3]);
+            }
+        }
+    } else {
+        for (int c = lane; c < cols; c += 64) s += bf16_to_f32(w[c]) * x[c];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane == 0) y[row] = s + (add ? add[row] : 0.f);
+}
+
+__global__ void k_silu(float* __restrict__ y, const float* __restrict__ x, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float v = x[i];
+        y[i] = v / (1.f + expf(-v));
+    }
+}
+
+// tok[t][f], f = 4c + 2m + nn: channel c (< 16; channel 16 is the all-zero padding mask), patch row m, column nn
+__global__ void k_patchify(float* __restrict__ tok, const float* __restrict__ lat, int Hl, int Wl) {
+    const int Wp = Wl / 2, T = (Hl / 2) * Wp;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)T * 68) return;
+    const int f = (int)(i % 68), t = (int)(i / 68);
+    const int c = f >> 2, m = (f >> 1) & 1, nn = f & 1;
+    const int yy = (t / Wp) * 2 + m, xx = (t % Wp) * 2 + nn;
+    tok[i] = c < 16 ? lat[((size_t)c * Hl + yy) * Wl + xx] : 0.f;
+}
+
+// tok[t][f], f = 32 p1 + 16 p2 + c
+__global__ void k_unpatchify(float* __restrict__ lat, const float* __restrict__ tok, int ldt, int Hl, int Wl) {
+    const int Wp = Wl / 2, T = (Hl / 2) * Wp;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)T * 64) return;
+    const int f = (int)(i & 63), t = (int)(i >> 6);
+    const int p1 = f >> 5, p2 = (f >> 4) & 1, c = f & 15;
+    const int yy = (t / Wp) * 2 + p1, xx = (t % Wp) * 2 + p2;
+    lat[((size_t)c * Hl + yy) * Wl + xx] = tok[(size_t)t * ldt + f];
+}
+
+// y [T, rows] (row stride ldy) = x [T, cols] (row stride ldx) W^T: 64 x 64 output tiles, k in chunks of 32 through
+// LDS, each thread 4 x 4 outputs in fp32.
+__global__ __launch_bounds__(256) void k_linear_f32(float* __restrict__ y, int ldy, const float* __restrict__ x,
+                                                    int ldx, const uint16_t* __restrict__ W, int T, int rows, int cols) {
+    __shared__ float xs[32][65];
+    __shared__ float ws[32][65];
+    const int t0 = blockIdx.y * 64, n0 = blockIdx.x * 64, tid = threadIdx.x;
+    const int tr = (tid >> 4) * 4, tc = (tid & 15) * 4;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < cols; k0 += 32) {
+        for (int e = tid; e < 64 * 32; e += 256) {
+            const int r = e >> 5, k = e & 31;
+            const int tt = t0 + r, nn = n0 + r, kk = k0 + k;
+            xs[k][r] = (tt < T && kk < cols) ? x[(size_t)tt * ldx + kk] : 0.f;
+            ws[k][r] = (nn < rows && kk < cols) ? bf16_to_f32(W[(size_t)nn * cols + kk]) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int k = 0; k < 32; k++) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a[i] = xs[k][tr + i];
+                b[i] = ws[k][tc + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tt = t0 + tr + i, nn = n0 + tc + j;
+            if (tt < T && nn < rows) y[(size_t)tt * ldy + nn] = acc[i][j];
+        }
+}
+
+__global__ void k_cfg_combine(float* __restrict__ v, const float* __restrict__ vn, float cfg, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) v[i] = vn[i] + cfg * (v[i] - vn[i]);
+}
+
+static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
+
+hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(k_matvec_bf16, dim3((rows + 3) / 4), dim3(256), 0, s, y, W, x, add, rows, cols);
+    return hipGetLastError();
+}
+hipError_t launch_silu(float* y, const float* x, size_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_silu, dim3(nblk(n)), dim3(256), 0, s, y, x, n);
+    return hipGetLastError();
+}
+hipError_t launch_patchify(float* tok, const float* lat, int Hl, int Wl, hipStream_t s) {
+    const size_t n = (size_t)(Hl / 2) * (Wl / 2) * 68;
+    hipLaunchKernelGGL(k_patchify, dim3(nblk(n)), dim3(256), 0, s, tok, lat, Hl, Wl);
+    return hipGetLastError();
+}
+hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int Wl, hipStream_t s) {
+    const size_t n = (size_t)(Hl / 2) * (Wl / 2) * 64;
+    hipLaunchKernelGGL(k_unpatchify, dim3(nblk(n)), dim3(256), 0, s, lat, tok, ldt, Hl, Wl);
+    return hipGetLastError();
+}
+hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* W, int T, int rows, int cols,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(k_linear_f32, dim3((rows + 63) / 64, (T + 63) / 64), dim3(256), 0, s, y, ldy, x, ldx, W, T,
+                       rows, cols);
+    return hipGetLastError();
+}
+hipError_t launch_cfg_combine(float* v, const float* vn, float cfg, size_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_cfg_combine, dim3(nblk(n)), dim3(256), 0, s, v, vn, cfg, n);
+    return hipGetLastError();
+}
+
+}  // namespace kiln

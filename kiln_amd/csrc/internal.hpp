@@ -75,6 +75,16 @@ hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s);
 size_t gemm16_prepped_bytes(int N, int K);
 hipError_t launch_gemm_wprep(uint16_t* wp, const uint16_t* w, int N, int K, bool src_bf16, hipStream_t s);
 
+// the DiT forward's passes around the blocks (dit_aux.hip)
+hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
+                              hipStream_t s);
+hipError_t launch_silu(float* y, const float* x, size_t n, hipStream_t s);
+hipError_t launch_patchify(float* tok, const float* lat, int Hl, int Wl, hipStream_t s);
+hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int Wl, hipStream_t s);
+hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* W, int T, int rows, int cols,
+                             hipStream_t s);
+hipError_t launch_cfg_combine(float* v, const float* vn, float cfg, size_t n, hipStream_t s);
+
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s);
 

@@ -19,10 +19,12 @@ and the MLP (engine/src/dit.cu:266-268, used at :460-493). Context K/V are prepa
 block (Dit::cache_context, engine/src/dit.cu:217-234): K = rmsnorm(ctx @ ca_k^T; ca_kn), V = ctx @ ca_v^T.
 Every call below goes to the HIP library; there is no CPU path.
 """
+import numpy as np
 import torch
 
 from . import (KILN_EPI_F32, KILN_EPI_GELU16, KILN_EPI_RESID, cross_attn_nag, dit_self_attn,
-               dit_self_attn_workspace_bytes, kv_prepare, layernorm_mod, linear16, linear16_prepare_weight)
+               dit_self_attn_workspace_bytes, kv_prepare, layernorm_mod, linear16, linear16_prepare_weight,
+               linear_f32, matvec, patchify, rmsnorm, silu, unpatchify)
 
 HD = 128
 
@@ -31,7 +33,8 @@ class Block16:
     """The weights of one DiT block in the layout the fp16 path consumes: every linear16 weight prepared at
     load (kiln_linear16_prepare_weight; Q/K/V stacked into one [3D, D] weight), norm weights bf16 [128]."""
 
-    def __init__(self, sa_qkv, sa_o, ca_q, ca_o, mlp1, mlp2, sa_qn, sa_kn, ca_qn, ca_kn, ca_k=None, ca_v=None):
+    def __init__(self, sa_qkv, sa_o, ca_q, ca_o, mlp1, mlp2, sa_qn, sa_kn, ca_qn, ca_kn, ca_k=None, ca_v=None,
+                 mod=None):
         self.sa_qkv = linear16_prepare_weight(sa_qkv)
         self.sa_o = linear16_prepare_weight(sa_o)
         self.ca_q = linear16_prepare_weight(ca_q)
@@ -40,6 +43,8 @@ class Block16:
         self.mlp2 = linear16_prepare_weight(mlp2)
         self.sa_qn, self.sa_kn, self.ca_qn, self.ca_kn = sa_qn, sa_kn, ca_qn, ca_kn
         self.ca_k, self.ca_v = ca_k, ca_v  # fp32 [D, Dctx] context projections (used by prepare_context)
+        # adaLN modulation weights, bf16: (sa1 [256, D], sa2 [3D, 256], ca1, ca2, mlp1, mlp2), dit.cu:266-268
+        self.mod = mod
         self.D = sa_o.shape[0]
         self.F = mlp1.shape[0]
 
@@ -91,3 +96,77 @@ def block_forward16(X, mods, blk, ws, B, T, rope, ctx, nag=None, eps=1e-6):
     linear16(ws.h16, ws.n16, blk.mlp1, epi=KILN_EPI_GELU16)
     linear16(X, ws.h16, blk.mlp2, epi=KILN_EPI_RESID, gate=mm[2 * D:3 * D])
     return X
+
+
+class StepWeights:
+    """The DiT's per-step weights outside the blocks, bf16 (engine/src/dit.cu:53-59, 242-272): the timestep MLP
+    t_lin1 [D, D], t_lin2 [3D, D] (the adaLN-LoRA vector), t_norm [D]; the final layer's modulation
+    final_mod1 [256, D], final_mod2 [2D, 256]; the patch embedder x_embed [D, 68] and final_lin [64, D]."""
+
+    def __init__(self, t_lin1, t_lin2, t_norm, final_mod1, final_mod2, x_embed, final_lin):
+        self.t_lin1, self.t_lin2, self.t_norm = t_lin1, t_lin2, t_norm
+        self.final_mod1, self.final_mod2 = final_mod1, final_mod2
+        self.x_embed, self.final_lin = x_embed, final_lin
+
+
+def timestep_sinusoid(t, D):
+    """The host-side sinusoid of Dit::step_tables (engine/src/dit.cu:246-251), fp32 arithmetic: cos(t e_i) and
+    sin(t e_i), e_i = exp(-i ln(10000) / (D/2))."""
+    i = np.arange(D // 2, dtype=np.float32)
+    e = np.exp(i * np.float32(-np.log(np.float32(10000.0))) / np.float32(D // 2)).astype(np.float32)
+    te = (np.float32(t) * e).astype(np.float32)
+    return np.concatenate([np.cos(te), np.sin(te)]).astype(np.float32)
+
+
+def step_tables(t, sw, blocks, device, eps=1e-6):
+    """Dit::step_tables (engine/src/dit.cu:242-272): the modulation vectors of every block ([9D] each) and of
+    the final layer ([2D]), from the timestep t. Returns (mods [nblocks, 9D], fmod [2D])."""
+    D = sw.t_lin1.shape[0]
+    s = torch.from_numpy(timestep_sinusoid(t, D)).to(device)
+    s1 = torch.empty(D, device=device)
+    lora = torch.empty(3 * D, device=device)
+    temb = torch.empty(D, device=device)
+    h = torch.empty(256, device=device)
+    matvec(s1, sw.t_lin1, s)
+    silu(s1, s1)
+    matvec(lora, sw.t_lin2, s1)
+    rmsnorm(temb, s, sw.t_norm, rows=1, dim=D, eps=eps)
+    silu(temb, temb)  # every modulation MLP starts with SiLU
+    mods = torch.empty(len(blocks), 9 * D, device=device)
+    for i, blk in enumerate(blocks):
+        for j in range(3):
+            matvec(h, blk.mod[2 * j], temb)
+            matvec(mods[i, 3 * j * D:3 * (j + 1) * D], blk.mod[2 * j + 1], h, add=lora)
+    fmod = torch.empty(2 * D, device=device)
+    matvec(h, sw.final_mod1, temb)
+    matvec(fmod, sw.final_mod2, h, add=lora[:2 * D])
+    return mods, fmod
+
+
+def forward16(outs, latent, t, sw, blocks, ws, B, rope, ctx, nag=None, eps=1e-6):
+    """Dit::forward_batch on the fp16 path (engine/src/dit.cu:357-546, without the step cache): every batch
+    item starts from the same latent [16, Hl, Wl]; outs: B latents [16, Hl, Wl] (the velocity predictions).
+    ctx[b] = (prepared K/V of block i -> list over blocks, real rows, padding rows); nag as in block_forward16
+    but with per-block prepared K/V lists."""
+    Hl, Wl = latent.shape[1], latent.shape[2]
+    T = (Hl // 2) * (Wl // 2)
+    D = sw.t_lin1.shape[0]
+    dev = latent.device
+    mods, fmod = step_tables(t, sw, blocks, dev, eps)
+    tok = torch.empty(T, 68, device=dev)
+    patchify(tok, latent)
+    X = torch.empty(B * T, D, device=dev)
+    linear_f32(X[:T], tok, sw.x_embed)
+    for b in range(1, B):
+        X[b * T:(b + 1) * T].copy_(X[:T])
+    for i, blk in enumerate(blocks):
+        cb = [(c[0][i], c[1], c[2]) for c in ctx]
+        nb = None if nag is None else (nag[0][i],) + tuple(nag[1:])
+        block_forward16(X, mods[i], blk, ws, B, T, rope, cb, nag=nb, eps=eps)
+    N = torch.empty_like(X)
+    layernorm_mod(N, X, fmod[D:2 * D], fmod[:D], eps)
+    y = torch.empty(B * T, 64, device=dev)
+    linear_f32(y, N, sw.final_lin)
+    for b in range(B):
+        unpatchify(outs[b], y[b * T:(b + 1) * T])
+    return outs

@@ -34,6 +34,10 @@ def lib():
         L.oracle_add_gated.argtypes = [_f32p, _f32p, ctypes.c_void_p, ctypes.c_long, _i]
         L.oracle_linear16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _i, _u16p, _i, _u16p, _i, _i, ctypes.c_void_p,
                                       ctypes.c_void_p, _i, _i, ctypes.c_void_p, ctypes.c_float]
+        L.oracle_matvec_bf16.argtypes = [_f32p, _u16p, _f32p, ctypes.c_void_p, _i, _i]
+        L.oracle_patchify.argtypes = [_f32p, _f32p, _i, _i]
+        L.oracle_unpatchify.argtypes = [_f32p, _f32p, _i, _i]
+        L.oracle_linear_f32.argtypes = [_f32p, _f32p, _u16p, _i, _i, _i]
         L.oracle_rope_half.argtypes = [_f32p, _i, _i, _i, _i, _f32p, _f32p]
         L.oracle_cosmos_rope.argtypes = [_f32p, _f32p, _i, _i]
         L.oracle_nag.argtypes = [_f32p, _i, _f32p, _i, _i, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float]
@@ -125,6 +129,40 @@ def linear16(x16, w16, epi=EPI_F32, y=None, gate=None, beta=0.0, a2=None, w2=Non
     lib().oracle_linear16(o32, o16, rows, x16, T, w16, rows, cols, a2.ctypes.data if k2 else None,
                           w2.ctypes.data if k2 else None, k2, epi, g.ctypes.data if g is not None else None, beta)
     return out
+
+
+def matvec_bf16(W, x, add=None):
+    """y = W x (+ add), W bf16 bit patterns (uint16) [rows, cols] (engine/src/kernels.cu k_matvec)."""
+    W = np.ascontiguousarray(W, dtype=np.uint16)
+    y = np.empty(W.shape[0], np.float32)
+    a = _c32(add) if add is not None else None
+    lib().oracle_matvec_bf16(y, W, _c32(x), a.ctypes.data if a is not None else None, W.shape[0], W.shape[1])
+    return y
+
+
+def patchify(lat):
+    """lat [16, Hl, Wl] -> tok [T, 68] (engine/src/dit.cu:174-182)."""
+    lat = _c32(lat)
+    Hl, Wl = lat.shape[1], lat.shape[2]
+    tok = np.empty(((Hl // 2) * (Wl // 2), 68), np.float32)
+    lib().oracle_patchify(tok, lat, Hl, Wl)
+    return tok
+
+
+def unpatchify(tok, Hl, Wl):
+    """tok [T, 64] -> lat [16, Hl, Wl] (engine/src/dit.cu:184-191)."""
+    lat = np.zeros((16, Hl, Wl), np.float32)
+    lib().oracle_unpatchify(lat, _c32(tok), Hl, Wl)
+    return lat
+
+
+def linear_f32(x, W):
+    """y = x W^T with W bf16 bit patterns [rows, cols] (engine/src/kernels.cu:508-529)."""
+    x = _c32(x)
+    W = np.ascontiguousarray(W, dtype=np.uint16)
+    y = np.empty((x.shape[0], W.shape[0]), np.float32)
+    lib().oracle_linear_f32(y, x, W, x.shape[0], W.shape[0], W.shape[1])
+    return y
 
 
 def rmsnorm_rows(x, w_bf16=None, eps=1e-6, dim=128):

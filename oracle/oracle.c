@@ -335,6 +335,56 @@ void oracle_linear16(float* y32, uint16_t* y16, int ldy, const uint16_t* x16, in
 }
 
 /*
+ * matvec with bf16 weights (engine/src/kernels.cu k_matvec, matvec at gpu.h:122): y[r] = sum_c W[r][c] x[c] (+ add[r]),
+ * accumulated in double. Pinned: equals numpy float64 W @ x on the bf16 values.
+ */
+void oracle_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        double s = 0.0;
+        for (int c = 0; c < cols; c++) s += (double)bf16_to_f32(W[(size_t)r * cols + c]) * x[c];
+        y[r] = (float)(s + (add ? add[r] : 0.0));
+    }
+}
+
+/*
+ * 2x2 patch embedding layout (engine/src/dit.cu:174-191). patchify: tok[t][4c + 2m + n] = lat[c][2(t / Wp) + m]
+ * [2(t % Wp) + n] for c < 16, 0 for the padding-mask channel c = 16. unpatchify: lat[c][2(t / Wp) + p1][2(t % Wp)
+ * + p2] = tok[t][32 p1 + 16 p2 + c]. Pinned: hand-computed positions; unpatchify of a patchify with the feature
+ * order mapped from (c, m, n) to (m, n, c) returns the latent.
+ */
+void oracle_patchify(float* tok, const float* lat, int Hl, int Wl) {
+    const int Wp = Wl / 2, T = (Hl / 2) * Wp;
+    for (int t = 0; t < T; t++)
+        for (int f = 0; f < 68; f++) {
+            const int c = f / 4, m = (f / 2) % 2, n = f % 2;
+            tok[(size_t)t * 68 + f] = c < 16 ? lat[((size_t)c * Hl + (t / Wp) * 2 + m) * Wl + (t % Wp) * 2 + n] : 0.f;
+        }
+}
+void oracle_unpatchify(float* lat, const float* tok, int Hl, int Wl) {
+    const int Wp = Wl / 2, T = (Hl / 2) * Wp;
+    for (int t = 0; t < T; t++)
+        for (int f = 0; f < 64; f++) {
+            const int p1 = f / 32, p2 = (f / 16) % 2, c = f % 16;
+            lat[((size_t)c * Hl + (t / Wp) * 2 + p1) * Wl + (t % Wp) * 2 + p2] = tok[(size_t)t * 64 + f];
+        }
+}
+
+/*
+ * fp32 linear layer with bf16 weights (engine/src/kernels.cu:508-529 linear, used for the x embedder and the final
+ * layer, dit.cu:417,542): y[t][n] = sum_k x[t][k] W[n][k], accumulated in double. Pinned: numpy float64 x @ W.T.
+ */
+void oracle_linear_f32(float* y, const float* x, const uint16_t* W, int T, int rows, int cols) {
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; t++)
+        for (int n = 0; n < rows; n++) {
+            double s = 0.0;
+            for (int k = 0; k < cols; k++) s += (double)x[(size_t)t * cols + k] * bf16_to_f32(W[(size_t)n * cols + k]);
+            y[(size_t)t * rows + n] = (float)s;
+        }
+}
+
+/*
  * Rotate-half RoPE (engine/src/kernels.cu:759-772, k_rope_half), in place on x [T, H*Dh]
  * (row stride ld elements), tables [T, Dh/2]:
  *   a = p[i], b = p[i+half];  p[i] = a*c - b*s;  p[i+half] = b*c + a*s

@@ -56,62 +56,169 @@ def _ln16(x, shift, scale, eps):
     return _r16((x - m) / torch.sqrt(var + eps) * (1 + scale) + shift)
 
 
-def test_dit_block_forward16_matches_reference(gpu):
-    H, Hp, Wp, B, Dctx, L = 4, 8, 12, 2, 256, 64
-    D, F, T, eps = H * HD, 4 * H * HD, Hp * Wp, 1e-6
-    g = torch.Generator().manual_seed(31)
+H, Hp, Wp, B, DCTX, L = 4, 8, 12, 2, 256, 64
+D, F, T, EPS = H * HD, 4 * H * HD, Hp * Wp, 1e-6
+REALS = [40, 64, 33]  # prompt, unconditional, NAG negative: real rows of 64-row contexts
+NAG = (5.0, 2.5, 0.25)
 
+
+def _make_block(g):
     def w16(o, i):
         return (torch.randn(o, i, generator=g) * i ** -0.5).half()
 
-    Wqkv, Wo, Wcq, Wco, W1, W2 = w16(3 * D, D), w16(D, D), w16(D, D), w16(D, D), w16(F, D), w16(D, F)
-    Wck, Wcv = torch.randn(D, Dctx, generator=g) * Dctx ** -0.5, torch.randn(D, Dctx, generator=g) * Dctx ** -0.5
-    nw = [_bf16(1 + 0.2 * torch.randn(HD, generator=g)) for _ in range(4)]  # sa_qn, sa_kn, ca_qn, ca_kn
+    w = dict(qkv=w16(3 * D, D), o=w16(D, D), cq=w16(D, D), co=w16(D, D), w1=w16(F, D), w2=w16(D, F),
+             ck=torch.randn(D, DCTX, generator=g) * DCTX ** -0.5, cv=torch.randn(D, DCTX, generator=g) * DCTX ** -0.5,
+             nw=[_bf16(1 + 0.2 * torch.randn(HD, generator=g)) for _ in range(4)])
+    blk = dit.Block16(w["qkv"].to(DEV), w["o"].to(DEV), w["cq"].to(DEV), w["co"].to(DEV), w["w1"].to(DEV),
+                      w["w2"].to(DEV), *[v.to(DEV) for v in w["nw"]], ca_k=w["ck"].to(DEV), ca_v=w["cv"].to(DEV))
+    return w, blk
+
+
+def _ref_block(x, mods, w, ctxs, rc, rs):
+    """float64 restatement of one block (engine/src/dit.cu:458-493), fp16 rounding where the fp16 path stores."""
+    d = lambda t: t.double()  # noqa: E731
+    nw = [d(v.float()) for v in w["nw"]]
+    mo, mc, mm = d(mods[:3 * D]), d(mods[3 * D:6 * D]), d(mods[6 * D:])
+    n = _ln16(x, mo[:D], mo[D:2 * D], EPS)
+    qkv = n @ d(w["qkv"]).T
+    a = torch.empty(B * T, D, dtype=torch.float64)
+    for b in range(B):
+        rows = slice(b * T, (b + 1) * T)
+        q = _rope(_rms(qkv[rows, :D], nw[0], H, EPS), d(rc), d(rs), H)
+        k = _rope(_rms(qkv[rows, D:2 * D], nw[1], H, EPS), d(rc), d(rs), H)
+        a[rows] = _r16(_attn(q, k, qkv[rows, 2 * D:], H))
+    x = x + mo[2 * D:] * (a @ d(w["o"]).T)
+    n = _ln16(x, mc[:D], mc[D:2 * D], EPS)
+    qc = _rms(n @ d(w["cq"]).T, nw[2], H, EPS)
+    kc = [_rms(d(c) @ d(w["ck"]).T, nw[3], H, EPS) for c in ctxs]
+    vc = [d(c) @ d(w["cv"]).T for c in ctxs]
+    for b in range(B):
+        rows = slice(b * T, (b + 1) * T)
+        a[rows] = _r16(_attn(qc[rows], kc[b], vc[b], H, L - REALS[b]))
+    an = _r16(_attn(qc[:T], kc[2], vc[2], H, L - REALS[2]))
+    a[:T] = _r16(torch.from_numpy(oracle.nag(a[:T].numpy(), an.numpy(), *NAG)).double())
+    x = x + mc[2 * D:] * (a @ d(w["co"]).T)
+    n = _ln16(x, mm[:D], mm[D:2 * D], EPS)
+    h = n @ d(w["w1"]).T
+    h = _r16(0.5 * h * (1 + torch.erf(h / np.sqrt(2))))
+    return x + mm[2 * D:] * (h @ d(w["w2"]).T)
+
+
+def test_dit_block_forward16_matches_reference(gpu):
+    g = torch.Generator().manual_seed(31)
+    w, blk = _make_block(g)
     mods = torch.randn(9 * D, generator=g) * 0.3
     X0 = torch.randn(B * T, D, generator=g)
-    reals = [40, 64, 33]  # prompt, unconditional, NAG negative: real rows of 64-row contexts
-    ctxs = [torch.randn(r, Dctx, generator=g) for r in reals]
-    nag = (5.0, 2.5, 0.25)
-
-    blk = dit.Block16(Wqkv.to(DEV), Wo.to(DEV), Wcq.to(DEV), Wco.to(DEV), W1.to(DEV), W2.to(DEV),
-                      *[w.to(DEV) for w in nw], ca_k=Wck.to(DEV), ca_v=Wcv.to(DEV))
-    kvs = [blk.prepare_context(c.to(DEV), eps) for c in ctxs]
+    ctxs = [torch.randn(r, DCTX, generator=g) for r in REALS]
+    kvs = [blk.prepare_context(c.to(DEV), EPS) for c in ctxs]
     rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
     ws = dit.Workspace(B, T, D, F, DEV)
     X = X0.to(DEV).clone()
     dit.block_forward16(X, mods.to(DEV), blk, ws, B, T, (rc.to(DEV), rs.to(DEV)),
-                        [(kvs[i], reals[i], L - reals[i]) for i in range(B)],
-                        nag=(kvs[2], reals[2], L - reals[2]) + nag, eps=eps)
+                        [(kvs[i], REALS[i], L - REALS[i]) for i in range(B)],
+                        nag=(kvs[2], REALS[2], L - REALS[2]) + NAG, eps=EPS)
     torch.cuda.synchronize()
-
-    # float64 restatement
-    d = lambda t: t.double()  # noqa: E731
-    x = d(X0)
-    mo, mc, mm = d(mods[:3 * D]), d(mods[3 * D:6 * D]), d(mods[6 * D:])
-    n = _ln16(x, mo[:D], mo[D:2 * D], eps)
-    qkv = n @ d(Wqkv).T
-    a = torch.empty(B * T, D, dtype=torch.float64)
-    for b in range(B):
-        rows = slice(b * T, (b + 1) * T)
-        q = _rope(_rms(qkv[rows, :D], d(nw[0].float()), H, eps), d(rc), d(rs), H)
-        k = _rope(_rms(qkv[rows, D:2 * D], d(nw[1].float()), H, eps), d(rc), d(rs), H)
-        a[rows] = _r16(_attn(q, k, qkv[rows, 2 * D:], H))
-    x = x + mo[2 * D:] * (a @ d(Wo).T)
-    n = _ln16(x, mc[:D], mc[D:2 * D], eps)
-    qc = _rms(n @ d(Wcq).T, d(nw[2].float()), H, eps)
-    kc = [_rms(d(c) @ d(Wck).T, d(nw[3].float()), H, eps) for c in ctxs]
-    vc = [d(c) @ d(Wcv).T for c in ctxs]
-    for b in range(B):
-        rows = slice(b * T, (b + 1) * T)
-        a[rows] = _r16(_attn(qc[rows], kc[b], vc[b], H, L - reals[b]))
-    an = _r16(_attn(qc[:T], kc[2], vc[2], H, L - reals[2]))
-    a[:T] = _r16(torch.from_numpy(oracle.nag(a[:T].numpy(), an.numpy(), *nag)).double())
-    x = x + mc[2 * D:] * (a @ d(Wco).T)
-    n = _ln16(x, mm[:D], mm[D:2 * D], eps)
-    h = n @ d(W1).T
-    h = _r16(0.5 * h * (1 + torch.erf(h / np.sqrt(2))))
-    x = x + mm[2 * D:] * (h @ d(W2).T)
-
+    x = _ref_block(X0.double(), mods, w, ctxs, rc, rs)
     err = (X.cpu().double() - x).abs()
     assert torch.isfinite(X).all()
     assert err.max().item() <= 1e-2 and err.mean().item() <= 5e-4, (err.max().item(), err.mean().item())
+
+
+def _bf16w(g, o, i, scale=None):
+    return _bf16(torch.randn(o, i, generator=g) * (scale if scale is not None else i ** -0.5))
+
+
+def test_dit_forward16_two_blocks_matches_reference(gpu):
+    """Dit::forward_batch on the fp16 path (engine/src/dit.cu:357-546) with two blocks: step tables (timestep
+    sinusoid, t_embedder MLP, adaLN modulation matvecs), patch embedding, the blocks, the final modulated
+    LayerNorm + linear and unpatchify, against a float64 restatement. Bar on the output latents (~N(0,1)):
+    max-abs 2e-2, mean-abs 1e-3."""
+    g = torch.Generator().manual_seed(32)
+    Hl, Wl, t = 2 * Hp, 2 * Wp, 0.73
+    blocks, ws_ = [], []
+    for _ in range(2):
+        w, blk = _make_block(g)
+        mod = [_bf16w(g, 256, D), _bf16w(g, 3 * D, 256), _bf16w(g, 256, D), _bf16w(g, 3 * D, 256),
+               _bf16w(g, 256, D), _bf16w(g, 3 * D, 256)]
+        blk.mod = [m.to(DEV) for m in mod]
+        w["mod"] = mod
+        blocks.append(blk)
+        ws_.append(w)
+    sw_h = dict(t_lin1=_bf16w(g, D, D), t_lin2=_bf16w(g, 3 * D, D), t_norm=_bf16(1 + 0.1 * torch.randn(D, generator=g)),
+                f1=_bf16w(g, 256, D), f2=_bf16w(g, 2 * D, 256), xe=_bf16w(g, D, 68, 68 ** -0.5), fl=_bf16w(g, 64, D))
+    sw = dit.StepWeights(*[sw_h[k].to(DEV) for k in ("t_lin1", "t_lin2", "t_norm", "f1", "f2", "xe", "fl")])
+    ctxs = [torch.randn(r, DCTX, generator=g) for r in REALS]
+    kv = [[blk.prepare_context(c.to(DEV), EPS) for blk in blocks] for c in ctxs]
+    latent = torch.randn(16, Hl, Wl, generator=g)
+    rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
+    ws = dit.Workspace(B, T, D, F, DEV)
+    outs = [torch.empty(16, Hl, Wl, device=DEV) for _ in range(B)]
+    dit.forward16(outs, latent.to(DEV), t, sw, blocks, ws, B, (rc.to(DEV), rs.to(DEV)),
+                  [(kv[i], REALS[i], L - REALS[i]) for i in range(B)], nag=(kv[2], REALS[2], L - REALS[2]) + NAG,
+                  eps=EPS)
+    torch.cuda.synchronize()
+
+    d = lambda a: a.double() if torch.is_tensor(a) else torch.from_numpy(a).double()  # noqa: E731
+    bw = lambda a: d(a.float())  # noqa: E731
+    silu = lambda v: v / (1 + torch.exp(-v))  # noqa: E731
+    s = d(dit.timestep_sinusoid(t, D))
+    lora = bw(sw_h["t_lin2"]) @ silu(bw(sw_h["t_lin1"]) @ s)
+    temb = silu(s / torch.sqrt((s * s).mean() + EPS) * bw(sw_h["t_norm"]))
+    tok = d(oracle.patchify(latent.numpy()))
+    x = (tok @ bw(sw_h["xe"]).T).repeat(B, 1)
+    for blk_w in ws_:
+        mods = torch.cat([bw(blk_w["mod"][2 * j + 1]) @ (bw(blk_w["mod"][2 * j]) @ temb) + lora for j in range(3)])
+        x = _ref_block(x, mods.float(), blk_w, ctxs, rc, rs)
+    fmod = bw(sw_h["f2"]) @ (bw(sw_h["f1"]) @ temb) + lora[:2 * D]
+    m = x.mean(-1, keepdim=True)
+    var = ((x - m) ** 2).mean(-1, keepdim=True)
+    n = (x - m) / torch.sqrt(var + EPS) * (1 + fmod[D:]) + fmod[:D]
+    y = n @ bw(sw_h["fl"]).T
+    for b in range(B):
+        ref = oracle.unpatchify(y[b * T:(b + 1) * T].float().numpy(), Hl, Wl).astype(np.float64)
+        err = np.abs(outs[b].cpu().double().numpy() - ref)
+        assert np.isfinite(err).all()
+        assert err.max() <= 2e-2 and err.mean() <= 1e-3, (b, err.max(), err.mean())
+
+
+@pytest.mark.parametrize("rows,cols", [(256, 2048), (6144, 256), (37, 100)])
+def test_matvec_bf16(gpu, rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    W = _bf16w(g, rows, cols, 1.0)
+    x, add = torch.randn(cols, generator=g), torch.randn(rows, generator=g)
+    y = torch.empty(rows, device=DEV)
+    kiln_amd.matvec(y, W.to(DEV), x.to(DEV), add=add.to(DEV))
+    ref = oracle.matvec_bf16(W.view(torch.int16).numpy().view(np.uint16), x.numpy(), add.numpy())
+    bar = np.sqrt(cols) * 2.0 ** -21 * (np.abs(W.float().numpy()) @ np.abs(x.numpy())) + 1e-6
+    assert (np.abs(y.cpu().numpy() - ref) <= bar).all()
+
+
+def test_linear_f32_patchify_silu_cfg(gpu):
+    g = torch.Generator().manual_seed(5)
+    Hl, Wl = 14, 22
+    lat = torch.randn(16, Hl, Wl, generator=g)
+    tok = torch.empty((Hl // 2) * (Wl // 2), 68, device=DEV)
+    kiln_amd.patchify(tok, lat.to(DEV))
+    np.testing.assert_array_equal(tok.cpu().numpy(), oracle.patchify(lat.numpy()))
+    y = torch.randn(tok.shape[0], 80, generator=g)  # row stride 80 >= 64
+    out = torch.full((16, Hl, Wl), float("nan"), device=DEV)
+    kiln_amd.unpatchify(out, y.to(DEV)[:, :64])
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.unpatchify(y[:, :64].contiguous().numpy(), Hl, Wl))
+    for T_, rows, cols in [(77, 2048, 68), (300, 64, 2048)]:
+        x = torch.randn(T_, cols, generator=g)
+        W = _bf16w(g, rows, cols)
+        yy = torch.empty(T_, rows, device=DEV)
+        kiln_amd.linear_f32(yy, x.to(DEV), W.to(DEV))
+        ref = oracle.linear_f32(x.numpy(), W.view(torch.int16).numpy().view(np.uint16))
+        bar = np.sqrt(cols) * 2.0 ** -21 * (np.abs(x.numpy()) @ np.abs(W.float().numpy()).T) + 1e-6
+        assert (np.abs(yy.cpu().numpy() - ref) <= bar).all()
+    v = torch.randn(1000, generator=g) * 4
+    sv = torch.empty(1000, device=DEV)
+    kiln_amd.silu(sv, v.to(DEV))
+    ref = (v.double() * torch.special.expit(v.double())).numpy()
+    np.testing.assert_allclose(sv.cpu().double().numpy(), ref, rtol=2e-6, atol=1e-7)
+    a, b = torch.randn(999, generator=g), torch.randn(999, generator=g)
+    ad = a.to(DEV)
+    kiln_amd.cfg_combine(ad, b.to(DEV), 4.5)
+    np.testing.assert_allclose(ad.cpu().numpy(), (b.double() + 4.5 * (a.double() - b.double())).numpy(), rtol=1e-6,
+                               atol=1e-6)

@@ -309,3 +309,38 @@ def test_linear16_gelu_special_values():
     got = oracle.linear16(xb.view(np.uint16), wb.view(np.uint16), oracle.EPI_GELU16).view(np.float16)[:, 0]
     ref = np.array([0.0, 0.8413447460685429, 12.0, 0.0, 4.0 * 0.9999683287581669], np.float64)
     np.testing.assert_array_equal(got, ref.astype(np.float16))
+
+
+def _bf16_bits(a):
+    """float32 -> bf16 bit patterns by truncation (exactly representable test weights)."""
+    return (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def _bf16_vals(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def test_matvec_and_linear_f32_match_numpy():
+    rng = np.random.default_rng(41)
+    W = _bf16_bits(rng.standard_normal((37, 200)))
+    x = rng.standard_normal(200).astype(np.float32)
+    add = rng.standard_normal(37).astype(np.float32)
+    np.testing.assert_allclose(oracle.matvec_bf16(W, x, add), _bf16_vals(W) @ x + add, rtol=1e-6, atol=1e-6)
+    X = rng.standard_normal((9, 200)).astype(np.float32)
+    np.testing.assert_allclose(oracle.linear_f32(X, W), X.astype(np.float64) @ _bf16_vals(W).T, rtol=1e-6, atol=1e-6)
+
+
+def test_patchify_positions_and_round_trip():
+    """Hand-computed positions (engine/src/dit.cu:174-191) and unpatchify o (patchify with its features reordered
+    from 4c + 2m + n to 32m + 16n + c) = identity."""
+    Hl, Wl = 6, 8
+    lat = np.random.default_rng(42).standard_normal((16, Hl, Wl)).astype(np.float32)
+    tok = oracle.patchify(lat)
+    assert tok.shape == (12, 68) and (tok[:, 64:] == 0).all()
+    # token t = 5 is patch row 1, column 1 (Wp = 4): pixel (2 + m, 2 + n); feature 4c + 2m + n
+    assert tok[5, 4 * 3 + 2 * 1 + 0] == lat[3, 3, 2]
+    assert tok[5, 4 * 15 + 1] == lat[15, 2, 3]
+    c, m, n = np.meshgrid(np.arange(16), np.arange(2), np.arange(2), indexing="ij")
+    reorder = np.zeros(64, np.int64)
+    reorder[(32 * m + 16 * n + c).ravel()] = (4 * c + 2 * m + n).ravel()
+    np.testing.assert_array_equal(oracle.unpatchify(tok[:, reorder], Hl, Wl), lat)

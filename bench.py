@@ -145,40 +145,46 @@ def dit_step_case(torch, kiln_amd, dev, nblocks=28, Hp=48, Wp=72, B=2, L=512, se
     return dict(T=T, step=step, flop=flop)
 
 
-def dit_blocks_case(torch, kiln_amd, dev, nblocks=28, ndistinct=4, Hp=48, Wp=72, B=2, L=512, seed=200):
-    """The 28 transformer blocks of a DiT step at config 5 on the fp16-activation path (kiln_amd.dit, the
-    reference's block loop engine/src/dit.cu:458-493): modulated LayerNorms, the Q/K/V, O, cross-Q, cross-O
-    and MLP linear16 GEMMs with their fused epilogues, fused self-attention, cross-attention + NAG. 2B shapes
-    (D = 2048, 16 heads, MLP 8192), random-init weights prepared at load; 4 distinct blocks cycled (472 MB of
-    weights, more than the 256 MB MALL, as 28 distinct blocks would be); contexts (positive, unconditional,
-    NAG negative) prepared per block outside the step. Not timed: the per-step modulation vectors (matvecs),
-    patch embedding and final layer (engine/src/dit.cu:242-272, 392-394, 537-544)."""
+def dit_forward_case(torch, kiln_amd, dev, nblocks=28, ndistinct=4, Hp=48, Wp=72, B=2, L=512, seed=200):
+    """One DiT forward of the CFG pair at config 5 on the fp16-activation path (kiln_amd.dit.forward16, the
+    reference's Dit::forward_batch, engine/src/dit.cu:357-546, without the step cache): step tables (timestep
+    MLP + the 28 blocks' adaLN matvecs), patch embedding, 28 blocks (modulated LayerNorms, the Q/K/V, O,
+    cross-Q, cross-O and MLP linear16 GEMMs with fused epilogues, fused self-attention, cross-attention +
+    NAG), final layer and unpatchify. 2B shapes (D = 2048, 16 heads, MLP 8192), random-init weights prepared
+    at load; 4 distinct blocks cycled (472 MB of weights, more than the 256 MB MALL, as 28 distinct blocks
+    would be); contexts (positive, unconditional, NAG negative, L = 512) prepared per block outside the step."""
     from kiln_amd import dit
     T, Dm = Hp * Wp, H * D
     g = torch.Generator(device=dev).manual_seed(seed)
     c, s = kiln_amd.cosmos_rope_tables(Hp, Wp)
     rope = (c.to(dev), s.to(dev))
     nw = torch.ones(D, dtype=torch.bfloat16, device=dev)
-    blocks = []
+
+    def bf(o, i):
+        return linear_init(torch, o, i, g, dev).to(torch.bfloat16)
+
+    distinct, ctx = [], [[], [], []]
     for _ in range(ndistinct):
         w = [linear_init(torch, o, i, g, dev).half() for o, i in
              [(3 * Dm, Dm), (Dm, Dm), (Dm, Dm), (Dm, Dm), (4 * Dm, Dm), (Dm, 4 * Dm)]]
         ck, cv = linear_init(torch, Dm, 1024, g, dev), linear_init(torch, Dm, 1024, g, dev)
-        blk = dit.Block16(*w, nw, nw, nw, nw, ca_k=ck, ca_v=cv)
+        blk = dit.Block16(*w, nw, nw, nw, nw, ca_k=ck, ca_v=cv,
+                          mod=[bf(256, Dm), bf(3 * Dm, 256), bf(256, Dm), bf(3 * Dm, 256), bf(256, Dm), bf(3 * Dm, 256)])
         del w
-        ctx = [blk.prepare_context(torch.randn(L, 1024, generator=g, device=dev)) for _ in range(3)]
-        mods = torch.randn(9 * Dm, generator=g, device=dev) * 0.1
-        blocks.append((blk, ctx, mods))
+        for j in range(3):
+            ctx[j].append(blk.prepare_context(torch.randn(L, 1024, generator=g, device=dev)))
+        distinct.append(blk)
+    blocks = [distinct[i % ndistinct] for i in range(nblocks)]
+    kv = [[ctx[j][i % ndistinct] for i in range(nblocks)] for j in range(3)]
+    sw = dit.StepWeights(bf(Dm, Dm), bf(3 * Dm, Dm), torch.ones(Dm, dtype=torch.bfloat16, device=dev), bf(256, Dm),
+                         bf(2 * Dm, 256), bf(Dm, 68), bf(64, Dm))
     ws = dit.Workspace(B, T, Dm, 4 * Dm, dev)
-    X = torch.randn(B * T, Dm, generator=g, device=dev)
-    X0 = X.clone()
+    latent = torch.randn(16, 2 * Hp, 2 * Wp, generator=g, device=dev)
+    outs = [torch.empty_like(latent) for _ in range(B)]
 
     def step():
-        X.copy_(X0)  # keeps the residual stream bounded over repeated steps (one 113 MB copy, ~25 us)
-        for i in range(nblocks):
-            blk, ctx, mods = blocks[i % ndistinct]
-            dit.block_forward16(X, mods, blk, ws, B, T, rope, [(ctx[0], L, 0), (ctx[1], L, 0)],
-                                nag=(ctx[2], L, 0, 5.0, 2.5, 0.25))
+        dit.forward16(outs, latent, 0.5, sw, blocks, ws, B, rope, [(kv[0], L, 0), (kv[1], L, 0)],
+                      nag=(kv[2], L, 0, 5.0, 2.5, 0.25))
 
     R = B * T
     gemm = 2.0 * R * Dm * Dm * 6 + 2 * 2.0 * R * 4 * Dm * Dm
@@ -397,10 +403,10 @@ def main():
 
     lin, blk_us, blk_fl = linear16_cases(torch, kiln_amd, tm, dev, args.steps, args.warmup)
 
-    cfgb = dit_blocks_case(torch, kiln_amd, dev)
+    cfgb = dit_forward_case(torch, kiln_amd, dev)
     ms_blk = tm.run(cfgb["step"], max(3, args.steps // 5), 1)
-    log(f"config 5, 28 DiT blocks on the fp16 path (LN + linear16 + attention + NAG): {ms_blk:.3f} ms per step  "
-        f"{cfgb['flop'] / ms_blk / 1e9:.1f} TFLOP/s")
+    log(f"config 5, DiT forward of the CFG pair on the fp16 path (step tables, embed, 28 blocks, final layer): "
+        f"{ms_blk:.3f} ms per step  {cfgb['flop'] / ms_blk / 1e9:.1f} TFLOP/s")
     cfgb_flop = cfgb["flop"]
     del cfgb
 
@@ -456,10 +462,11 @@ def main():
             "linear16_torch_f16out_tflops": {k: round(v["torch_tflops"], 1) for k, v in lin.items()},
             "linear16_dit_block_us": round(blk_us, 1),
             "linear16_dit_block_tflops": round(blk_fl / blk_us / 1e6, 1),
-            "dit_28_blocks_ms_per_step": round(ms_blk, 3),
-            "dit_28_blocks_tflops": round(cfgb_flop / ms_blk / 1e9, 1),
-            "dit_28_blocks_workload": "config 5: 28 x (3 LN16 + Q/K/V, O, cross-Q, cross-O, MLP linear16 + self-attn + "
-                                      "cross-attn L=512 + NAG), B=2, T=3456, 2B shapes, fp16 path",
+            "dit_forward_ms_per_step": round(ms_blk, 3),
+            "dit_forward_tflops": round(cfgb_flop / ms_blk / 1e9, 1),
+            "dit_forward_workload": "config 5: Dit::forward_batch of the CFG pair on the fp16 path (step tables, patch "
+                                    "embed, 28 x (3 LN16 + Q/K/V, O, cross-Q, cross-O, MLP linear16 + self-attn + "
+                                    "cross-attn L=512 + NAG), final layer), B=2, T=3456, 2B shapes",
         },
         "roofline": {
             "bound": "mfma",

@@ -138,6 +138,11 @@ int kiln_linear16_prepped(void* y, int ldy, const uint16_t* x16, int T, const ui
  * [rows, cols] row-major, x fp32 [cols], add fp32 [rows] or NULL. The per-step modulation vectors. */
 int kiln_matvec_bf16(float* y, const uint16_t* w_bf16, const float* x, const float* add, int rows, int cols,
                      kiln_stream_t stream);
+/* groups matvecs in one launch (the per-block adaLN second layers of Dit::step_tables, engine/src/dit.cu:266-268):
+ * y[g*rows + r] = sum_c W[g*rows + r][c] x[g*cols + c] (+ add[r]); W bf16 [groups*rows, cols] (the groups' weights
+ * stacked), x fp32 [groups, cols], add fp32 [rows] shared by every group (the adaLN-LoRA vector) or NULL. */
+int kiln_matvec_bf16_grouped(float* y, const uint16_t* w_bf16, const float* x, const float* add, int groups, int rows,
+                             int cols, kiln_stream_t stream);
 /* Replaces silu() (engine/src/gpu.h:142, kernels.cu:735-739): y = x / (1 + exp(-x)), n elements, in place
  * allowed. */
 int kiln_silu(float* y, const float* x, size_t n, kiln_stream_t stream);

@@ -38,6 +38,7 @@ _SIGS = {
     "kiln_add_gated": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "kiln_linear16": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "kiln_matvec_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "kiln_matvec_bf16_grouped": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "kiln_silu": (_i, [_vp, _vp, _sz, _vp]),
     "kiln_patchify": (_i, [_vp, _vp, _i, _i, _vp]),
     "kiln_unpatchify": (_i, [_vp, _vp, _i, _i, _i, _vp]),
@@ -333,6 +334,13 @@ def matvec(y, w_bf16, x, add=None, stream=None):
     """matvec (engine/src/gpu.h:122): y = W x (+ add), W bf16 [rows, cols]."""
     _check(lib().kiln_matvec_bf16(_ptr(y), _ptr(w_bf16), _ptr(x), _ptr(add), w_bf16.shape[0], w_bf16.shape[1],
                                   _stream(stream)))
+    return y
+
+
+def matvec_grouped(y, w_bf16, x, add=None, stream=None):
+    """groups matvecs in one launch: w_bf16 [groups, rows, cols], x [groups, cols], y [groups, rows], add [rows]."""
+    G, rows, cols = w_bf16.shape
+    _check(lib().kiln_matvec_bf16_grouped(_ptr(y), _ptr(w_bf16), _ptr(x), _ptr(add), G, rows, cols, _stream(stream)))
     return y
 
 

@@ -491,7 +491,17 @@ int kiln_matvec_bf16(float* y, const uint16_t* w_bf16, const float* x, const flo
     if (rows < 0 || cols <= 0) return fail(KILN_EINVAL, "matvec: bad sizes rows=%d cols=%d", rows, cols);
     if (rows && (!y || !w_bf16 || !x)) return fail(KILN_EINVAL, "matvec: null pointer");
     if (!rows) return KILN_OK;
-    return hip_check(kiln::launch_matvec_bf16(y, w_bf16, x, add, rows, cols, (hipStream_t)stream), "matvec launch");
+    return hip_check(kiln::launch_matvec_bf16(y, w_bf16, x, add, rows, cols, 1, (hipStream_t)stream), "matvec launch");
+}
+
+int kiln_matvec_bf16_grouped(float* y, const uint16_t* w_bf16, const float* x, const float* add, int groups, int rows,
+                             int cols, kiln_stream_t stream) {
+    if (groups < 0 || rows < 0 || cols <= 0 || (long)groups * rows > (1L << 30))
+        return fail(KILN_EINVAL, "matvec_grouped: bad sizes groups=%d rows=%d cols=%d", groups, rows, cols);
+    if (!groups || !rows) return KILN_OK;
+    if (!y || !w_bf16 || !x) return fail(KILN_EINVAL, "matvec_grouped: null pointer");
+    return hip_check(kiln::launch_matvec_bf16(y, w_bf16, x, add, rows, cols, groups, (hipStream_t)stream),
+                     "matvec_grouped launch");
 }
 
 int kiln_silu(float* y, const float* x, size_t n, kiln_stream_t stream) {

@@ -14,12 +14,15 @@
 
 namespace kiln {
 
-// One wave per row: 16-byte bf16 loads striding the row, fp32 partial sums, a wave reduction.
+// One wave per row: 16-byte bf16 loads striding the row, fp32 partial sums, a wave reduction. Grouped form:
+// rows [g*grows, (g+1)*grows) read input vector x + g*xstride and add[row - g*grows] (xstride = 0: one x).
 __global__ __launch_bounds__(256) void k_matvec_bf16(float* __restrict__ y, const uint16_t* __restrict__ W,
                                                      const float* __restrict__ x, const float* __restrict__ add,
-                                                     int rows, int cols) {
+                                                     int rows, int cols, int grows, int xstride) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
+    const int grp = row / grows;
+    x += (size_t)grp * xstride;
     const uint16_t* w = W + (size_t)row * cols;
     float s = 0.f;
     if ((cols & 7) == 0 && ((size_t)w & 15) == 0 && ((size_t)x & 15) == 0) {
@@ -38,7 +41,7 @@ __global__ __launch_bounds__(256) void k_matvec_bf16(float* __restrict__ y, cons
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    if (lane == 0) y[row] = s + (add ? add[row] : 0.f);
+    if (lane == 0) y[row] = s + (add ? add[row - grp * grows] : 0.f);
 }
 
 __global__ void k_silu(float* __restrict__ y, const float* __restrict__ x, size_t n) {
@@ -120,8 +123,10 @@ __global__ void k_cfg_combine(float* __restrict__ v, const float* __restrict__ v
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
-                              hipStream_t s) {
-    hipLaunchKernelGGL(k_matvec_bf16, dim3((rows + 3) / 4), dim3(256), 0, s, y, W, x, add, rows, cols);
+                              int groups, hipStream_t s) {
+    const int grows = rows, xstride = groups > 1 ? cols : 0;
+    hipLaunchKernelGGL(k_matvec_bf16, dim3((rows * groups + 3) / 4), dim3(256), 0, s, y, W, x, add, rows * groups,
+                       cols, grows, xstride);
     return hipGetLastError();
 }
 hipError_t launch_silu(float* y, const float* x, size_t n, hipStream_t s) {

@@ -76,8 +76,10 @@ size_t gemm16_prepped_bytes(int N, int K);
 hipError_t launch_gemm_wprep(uint16_t* wp, const uint16_t* w, int N, int K, bool src_bf16, hipStream_t s);
 
 // the DiT forward's passes around the blocks (dit_aux.hip)
+// groups > 1: W is groups stacked [rows, cols] matrices, x groups stacked [cols] vectors, y [groups * rows],
+// add [rows] shared by every group
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
-                              hipStream_t s);
+                              int groups, hipStream_t s);
 hipError_t launch_silu(float* y, const float* x, size_t n, hipStream_t s);
 hipError_t launch_patchify(float* tok, const float* lat, int Hl, int Wl, hipStream_t s);
 hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int Wl, hipStream_t s);

@@ -24,7 +24,7 @@ import torch
 
 from . import (KILN_EPI_F32, KILN_EPI_GELU16, KILN_EPI_RESID, cross_attn_nag, dit_self_attn,
                dit_self_attn_workspace_bytes, kv_prepare, layernorm_mod, linear16, linear16_prepare_weight,
-               linear_f32, matvec, patchify, rmsnorm, silu, unpatchify)
+               linear_f32, matvec, matvec_grouped, patchify, rmsnorm, silu, unpatchify)
 
 HD = 128
 
@@ -107,6 +107,7 @@ class StepWeights:
         self.t_lin1, self.t_lin2, self.t_norm = t_lin1, t_lin2, t_norm
         self.final_mod1, self.final_mod2 = final_mod1, final_mod2
         self.x_embed, self.final_lin = x_embed, final_lin
+        self._mod1 = None  # the blocks' modulation weights stacked for step_tables (built on first use)
 
 
 def timestep_sinusoid(t, D):
@@ -132,11 +133,16 @@ def step_tables(t, sw, blocks, device, eps=1e-6):
     matvec(lora, sw.t_lin2, s1)
     rmsnorm(temb, s, sw.t_norm, rows=1, dim=D, eps=eps)
     silu(temb, temb)  # every modulation MLP starts with SiLU
+    # every block's three modulation MLPs in two launches: [nblocks*3*256, D] first layers on temb, then the
+    # second layers [nblocks*3, 3D, 256] each on its own hidden vector, + lora
+    if getattr(sw, "_mod1", None) is None or sw._mod_blocks != [id(b) for b in blocks]:
+        sw._mod1 = torch.cat([blk.mod[2 * j] for blk in blocks for j in range(3)]).contiguous()
+        sw._mod2 = torch.stack([blk.mod[2 * j + 1] for blk in blocks for j in range(3)]).contiguous()
+        sw._mod_blocks = [id(b) for b in blocks]
+    hid = torch.empty(len(blocks) * 3, 256, device=device)
+    matvec(hid.view(-1), sw._mod1, temb)
     mods = torch.empty(len(blocks), 9 * D, device=device)
-    for i, blk in enumerate(blocks):
-        for j in range(3):
-            matvec(h, blk.mod[2 * j], temb)
-            matvec(mods[i, 3 * j * D:3 * (j + 1) * D], blk.mod[2 * j + 1], h, add=lora)
+    matvec_grouped(mods.view(len(blocks) * 3, 3 * D), sw._mod2, hid, add=lora)
     fmod = torch.empty(2 * D, device=device)
     matvec(h, sw.final_mod1, temb)
     matvec(fmod, sw.final_mod2, h, add=lora[:2 * D])

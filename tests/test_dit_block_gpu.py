@@ -222,3 +222,18 @@ def test_linear_f32_patchify_silu_cfg(gpu):
     kiln_amd.cfg_combine(ad, b.to(DEV), 4.5)
     np.testing.assert_allclose(ad.cpu().numpy(), (b.double() + 4.5 * (a.double() - b.double())).numpy(), rtol=1e-6,
                                atol=1e-6)
+
+
+def test_matvec_bf16_grouped(gpu):
+    """The grouped form (the adaLN second layers of all blocks in one launch) equals per-group matvecs."""
+    g = torch.Generator().manual_seed(77)
+    G_, rows, cols = 6, 384, 256
+    W = _bf16w(g, G_ * rows, cols, 1.0).view(G_, rows, cols)
+    x, add = torch.randn(G_, cols, generator=g), torch.randn(rows, generator=g)
+    y = torch.empty(G_, rows, device=DEV)
+    kiln_amd.matvec_grouped(y, W.to(DEV), x.to(DEV), add=add.to(DEV))
+    Wb = W.view(torch.int16).numpy().view(np.uint16)
+    for i in range(G_):
+        ref = oracle.matvec_bf16(Wb[i], x[i].numpy(), add.numpy())
+        bar = np.sqrt(cols) * 2.0 ** -21 * (np.abs(W[i].float().numpy()) @ np.abs(x[i].numpy())) + 1e-6
+        assert (np.abs(y[i].cpu().numpy() - ref) <= bar).all()

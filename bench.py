@@ -186,10 +186,21 @@ def dit_forward_case(torch, kiln_amd, dev, nblocks=28, ndistinct=4, Hp=48, Wp=72
         dit.forward16(outs, latent, 0.5, sw, blocks, ws, B, rope, [(kv[0], L, 0), (kv[1], L, 0)],
                       nag=(kv[2], L, 0, 5.0, 2.5, 0.25))
 
+    from kiln_amd import sampler
+    noise = torch.randn_like(latent)
+    x = torch.empty_like(latent)
+
+    def model(o, xx, t, cfg_now):  # the CFG pair in one batched forward (NAG on the prompt item)
+        dit.forward16(o, xx, t, sw, blocks, ws, B, rope, [(kv[0], L, 0), (kv[1], L, 0)],
+                      nag=(kv[2], L, 0, 5.0, 2.5, 0.25))
+
+    def sample8():  # 8 Euler steps, shift 3, CFG 4.5 on every step, timestep = sigma (multiplier 1)
+        sampler.sample_euler(model, x, noise, sampler.flow_sigmas(8, 3.0), cfg=4.5)
+
     R = B * T
     gemm = 2.0 * R * Dm * Dm * 6 + 2 * 2.0 * R * 4 * Dm * Dm
     attn = 4.0 * B * H * T * T * D + 4.0 * (B + 1) * H * T * L * D
-    return dict(step=step, flop=nblocks * (gemm + attn))
+    return dict(step=step, sample8=sample8, flop=nblocks * (gemm + attn))
 
 
 def linear16_cases(torch, kiln_amd, tm, dev, steps, warmup):
@@ -408,6 +419,8 @@ def main():
     log(f"config 5, DiT forward of the CFG pair on the fp16 path (step tables, embed, 28 blocks, final layer): "
         f"{ms_blk:.3f} ms per step  {cfgb['flop'] / ms_blk / 1e9:.1f} TFLOP/s")
     cfgb_flop = cfgb["flop"]
+    ms_s8 = tm.run(cfgb["sample8"], 2, 1)
+    log(f"config 5, 8-step Euler sampling with CFG 4.5 + NAG (8 forwards of the CFG pair): {ms_s8:.1f} ms")
     del cfgb
 
     traffic = None  # HBM bytes per launch of k_attn_fwd (config 4), from the committed rocprofv3 FETCH/WRITE runs
@@ -464,6 +477,7 @@ def main():
             "linear16_dit_block_tflops": round(blk_fl / blk_us / 1e6, 1),
             "dit_forward_ms_per_step": round(ms_blk, 3),
             "dit_forward_tflops": round(cfgb_flop / ms_blk / 1e9, 1),
+            "dit_sample_8_steps_ms": round(ms_s8, 1),
             "dit_forward_workload": "config 5: Dit::forward_batch of the CFG pair on the fp16 path (step tables, patch "
                                     "embed, 28 x (3 LN16 + Q/K/V, O, cross-Q, cross-O, MLP linear16 + self-attn + "
                                     "cross-attn L=512 + NAG), final layer), B=2, T=3456, 2B shapes",

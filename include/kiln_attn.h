@@ -158,6 +158,12 @@ int kiln_unpatchify(float* latent, const float* tok, int ldt, int Hl, int Wl, ki
  * W bf16 [rows, cols], fp32 arithmetic. */
 int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* w_bf16, int T, int rows, int cols,
                     kiln_stream_t stream);
+/* Flow-matching sampler start (engine/src/pipeline.cu:304-307, k_start): x = sigma * noise + (1 - sigma) * init
+ * (init NULL: 0), n elements. */
+int kiln_flow_start(float* x, const float* noise, const float* init, float sigma, size_t n, kiln_stream_t stream);
+/* One Euler step of the velocity v without a mask (engine/src/pipeline.cu:318-331, k_denoised then
+ * k_euler_step): den = x - v * sigma; x = x + (x - den) / sigma * (sigma_next - sigma). sigma > 0. */
+int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next, size_t n, kiln_stream_t stream);
 /* Replaces cfg_combine() (engine/src/gpu.h:144, kernels.cu:1058-1062): v = vn + cfg * (v - vn), n elements. */
 int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream_t stream);
 

@@ -44,6 +44,8 @@ _SIGS = {
     "kiln_unpatchify": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "kiln_linear_f32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
     "kiln_cfg_combine": (_i, [_vp, _vp, _f, _sz, _vp]),
+    "kiln_flow_start": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
+    "kiln_flow_euler_step": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "kiln_linear16_prepped_weight_bytes": (_sz, [_i, _i]),
     "kiln_linear16_prepare_weight": (_i, [_vp, _vp, _i, _i, _i, _vp]),
@@ -374,3 +376,15 @@ def cfg_combine(v, vn, cfg, stream=None):
     """cfg_combine (engine/src/kernels.cu:1058-1062): v = vn + cfg (v - vn)."""
     _check(lib().kiln_cfg_combine(_ptr(v), _ptr(vn), cfg, v.numel(), _stream(stream)))
     return v
+
+
+def flow_start(x, noise, sigma, init=None, stream=None):
+    """k_start (engine/src/pipeline.cu:304-307): x = sigma noise + (1 - sigma) init."""
+    _check(lib().kiln_flow_start(_ptr(x), _ptr(noise), _ptr(init), sigma, x.numel(), _stream(stream)))
+    return x
+
+
+def flow_euler_step(x, v, sigma, sigma_next, stream=None):
+    """k_denoised + k_euler_step (engine/src/pipeline.cu:318-331) without a mask, in place on x."""
+    _check(lib().kiln_flow_euler_step(_ptr(x), _ptr(v), sigma, sigma_next, x.numel(), _stream(stream)))
+    return x

@@ -539,6 +539,19 @@ int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream
     return hip_check(kiln::launch_cfg_combine(v, vn, cfg, n, (hipStream_t)stream), "cfg_combine launch");
 }
 
+int kiln_flow_start(float* x, const float* noise, const float* init, float sigma, size_t n, kiln_stream_t stream) {
+    if (n && (!x || !noise)) return fail(KILN_EINVAL, "flow_start: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_flow_start(x, noise, init, sigma, n, (hipStream_t)stream), "flow_start launch");
+}
+
+int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next, size_t n, kiln_stream_t stream) {
+    if (n && (!x || !v)) return fail(KILN_EINVAL, "flow_euler_step: null pointer");
+    if (!(sigma > 0.f)) return fail(KILN_EINVAL, "flow_euler_step: sigma %g must be > 0", (double)sigma);
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_flow_euler(x, v, sigma, sigma_next, n, (hipStream_t)stream), "flow_euler launch");
+}
+
 int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {
     if (T < 0 || H <= 0 || Dh <= 0 || Dh % 2) return fail(KILN_EINVAL, "bad sizes");
     if (T && (!x || !cos_t || !sin_t)) return fail(KILN_EINVAL, "null pointer");

@@ -120,6 +120,21 @@ __global__ void k_cfg_combine(float* __restrict__ v, const float* __restrict__ v
     if (i < n) v[i] = vn[i] + cfg * (v[i] - vn[i]);
 }
 
+// flow-matching sampler (engine/src/pipeline.cu:304-331): the start x = s noise + (1 - s) init, and one Euler step
+// of the velocity v in the reference's arithmetic: den = x - v s, then x + (x - den) / s (sn - s)
+__global__ void k_flow_start(float* __restrict__ x, const float* __restrict__ noise, const float* __restrict__ init,
+                             float s, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = s * noise[i] + (init ? (1.f - s) * init[i] : 0.f);
+}
+__global__ void k_flow_euler(float* __restrict__ x, const float* __restrict__ v, float s, float sn, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float xi = x[i], den = xi - v[i] * s;
+        x[i] = xi + (xi - den) / s * (sn - s);
+    }
+}
+
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
@@ -151,6 +166,15 @@ hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const u
 }
 hipError_t launch_cfg_combine(float* v, const float* vn, float cfg, size_t n, hipStream_t s) {
     hipLaunchKernelGGL(k_cfg_combine, dim3(nblk(n)), dim3(256), 0, s, v, vn, cfg, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_flow_start(float* x, const float* noise, const float* init, float s, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_start, dim3(nblk(n)), dim3(256), 0, st, x, noise, init, s, n);
+    return hipGetLastError();
+}
+hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_euler, dim3(nblk(n)), dim3(256), 0, st, x, v, s, sn, n);
     return hipGetLastError();
 }
 

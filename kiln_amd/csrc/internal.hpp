@@ -86,6 +86,8 @@ hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int 
 hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* W, int T, int rows, int cols,
                              hipStream_t s);
 hipError_t launch_cfg_combine(float* v, const float* vn, float cfg, size_t n, hipStream_t s);
+hipError_t launch_flow_start(float* x, const float* noise, const float* init, float s, size_t n, hipStream_t st);
+hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st);
 
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s);

@@ -158,6 +158,10 @@ int kiln_unpatchify(float* latent, const float* tok, int ldt, int Hl, int Wl, ki
  * W bf16 [rows, cols], fp32 arithmetic. */
 int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* w_bf16, int T, int rows, int cols,
                     kiln_stream_t stream);
+/* First-block step cache (engine/src/dit.cu:327-340, used at :404-433): y = a - b (k_sub), and the two sums of
+ * the relative L1 change, acc[0] = sum |a - b|, acc[1] = sum |b| (device float[2], overwritten; k_rel_l1). */
+int kiln_sub(float* y, const float* a, const float* b, size_t n, kiln_stream_t stream);
+int kiln_rel_l1(const float* a, const float* b, size_t n, float* acc, kiln_stream_t stream);
 /* Flow-matching sampler start (engine/src/pipeline.cu:304-307, k_start): x = sigma * noise + (1 - sigma) * init
  * (init NULL: 0), n elements. */
 int kiln_flow_start(float* x, const float* noise, const float* init, float sigma, size_t n, kiln_stream_t stream);

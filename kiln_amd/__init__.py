@@ -44,6 +44,8 @@ _SIGS = {
     "kiln_unpatchify": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "kiln_linear_f32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
     "kiln_cfg_combine": (_i, [_vp, _vp, _f, _sz, _vp]),
+    "kiln_sub": (_i, [_vp, _vp, _vp, _sz, _vp]),
+    "kiln_rel_l1": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "kiln_flow_start": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
     "kiln_flow_euler_step": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
@@ -388,3 +390,15 @@ def flow_euler_step(x, v, sigma, sigma_next, stream=None):
     """k_denoised + k_euler_step (engine/src/pipeline.cu:318-331) without a mask, in place on x."""
     _check(lib().kiln_flow_euler_step(_ptr(x), _ptr(v), sigma, sigma_next, x.numel(), _stream(stream)))
     return x
+
+
+def sub(y, a, b, stream=None):
+    """k_sub (engine/src/dit.cu:337-340): y = a - b."""
+    _check(lib().kiln_sub(_ptr(y), _ptr(a), _ptr(b), a.numel(), _stream(stream)))
+    return y
+
+
+def rel_l1(a, b, acc, stream=None):
+    """k_rel_l1 (engine/src/dit.cu:327-335): acc[0] = sum|a - b|, acc[1] = sum|b| (device float[2])."""
+    _check(lib().kiln_rel_l1(_ptr(a), _ptr(b), a.numel(), _ptr(acc), _stream(stream)))
+    return acc

@@ -539,6 +539,17 @@ int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream
     return hip_check(kiln::launch_cfg_combine(v, vn, cfg, n, (hipStream_t)stream), "cfg_combine launch");
 }
 
+int kiln_sub(float* y, const float* a, const float* b, size_t n, kiln_stream_t stream) {
+    if (n && (!y || !a || !b)) return fail(KILN_EINVAL, "sub: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_sub(y, a, b, n, (hipStream_t)stream), "sub launch");
+}
+
+int kiln_rel_l1(const float* a, const float* b, size_t n, float* acc, kiln_stream_t stream) {
+    if (!acc || (n && (!a || !b))) return fail(KILN_EINVAL, "rel_l1: null pointer");
+    return hip_check(kiln::launch_rel_l1(a, b, n, acc, (hipStream_t)stream), "rel_l1 launch");
+}
+
 int kiln_flow_start(float* x, const float* noise, const float* init, float sigma, size_t n, kiln_stream_t stream) {
     if (n && (!x || !noise)) return fail(KILN_EINVAL, "flow_start: null pointer");
     if (!n) return KILN_OK;

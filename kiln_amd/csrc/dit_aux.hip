@@ -135,6 +135,33 @@ __global__ void k_flow_euler(float* __restrict__ x, const float* __restrict__ v,
     }
 }
 
+// first-block step cache (engine/src/dit.cu:327-340): y = a - b, and the relative L1 change sum|a - b| / sum|b|
+// as two sums (acc[0], acc[1]) that the host divides
+__global__ void k_sub(float* __restrict__ y, const float* __restrict__ a, const float* __restrict__ b, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = a[i] - b[i];
+}
+__global__ void k_zero2(float* acc) {
+    if (threadIdx.x < 2) acc[threadIdx.x] = 0.f;
+}
+__global__ __launch_bounds__(256) void k_rel_l1(const float* __restrict__ a, const float* __restrict__ b, size_t n,
+                                                float* acc) {
+    float d = 0.f, r = 0.f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        d += fabsf(a[i] - b[i]);
+        r += fabsf(b[i]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        d += __shfl_xor(d, o, 64);
+        r += __shfl_xor(r, o, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        atomicAdd(acc, d);
+        atomicAdd(acc + 1, r);
+    }
+}
+
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
@@ -175,6 +202,16 @@ hipError_t launch_flow_start(float* x, const float* noise, const float* init, fl
 }
 hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(k_flow_euler, dim3(nblk(n)), dim3(256), 0, st, x, v, s, sn, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_sub(float* y, const float* a, const float* b, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_sub, dim3(nblk(n)), dim3(256), 0, st, y, a, b, n);
+    return hipGetLastError();
+}
+hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, hipStream_t st) {
+    hipLaunchKernelGGL(k_zero2, dim3(1), dim3(64), 0, st, acc);
+    hipLaunchKernelGGL(k_rel_l1, dim3(512), dim3(256), 0, st, a, b, n, acc);
     return hipGetLastError();
 }
 

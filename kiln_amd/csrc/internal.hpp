@@ -86,6 +86,8 @@ hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int 
 hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* W, int T, int rows, int cols,
                              hipStream_t s);
 hipError_t launch_cfg_combine(float* v, const float* vn, float cfg, size_t n, hipStream_t s);
+hipError_t launch_sub(float* y, const float* a, const float* b, size_t n, hipStream_t st);
+hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, hipStream_t st);
 hipError_t launch_flow_start(float* x, const float* noise, const float* init, float s, size_t n, hipStream_t st);
 hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st);
 

@@ -24,7 +24,7 @@ import torch
 
 from . import (KILN_EPI_F32, KILN_EPI_GELU16, KILN_EPI_RESID, cross_attn_nag, dit_self_attn,
                dit_self_attn_workspace_bytes, kv_prepare, layernorm_mod, linear16, linear16_prepare_weight,
-               linear_f32, matvec, matvec_grouped, patchify, rmsnorm, silu, unpatchify)
+               add_gated, linear_f32, matvec, matvec_grouped, patchify, rel_l1, rmsnorm, silu, sub, unpatchify)
 
 HD = 128
 
@@ -149,8 +149,20 @@ def step_tables(t, sw, blocks, device, eps=1e-6):
     return mods, fmod
 
 
-def forward16(outs, latent, t, sw, blocks, ws, B, rope, ctx, nag=None, eps=1e-6):
-    """Dit::forward_batch on the fp16 path (engine/src/dit.cu:357-546, without the step cache): every batch
+class StepCache:
+    """The first-block step cache (Dit::StepCache, engine/src/models.h:66-76): across the steps of one sampling
+    run, when block 0's residual moved less than `threshold` (relative L1) since the last full forward, the
+    forward reuses that forward's residual of blocks 1..N-1 instead of running them. `allow` is set per step by
+    the sampler."""
+
+    def __init__(self, threshold):
+        self.threshold, self.allow, self.valid, self.skipped = threshold, False, False, False
+        self.R, self.r0, self.resid, self.last_change = 0, None, None, 0.0
+        self.acc = None
+
+
+def forward16(outs, latent, t, sw, blocks, ws, B, rope, ctx, nag=None, eps=1e-6, sc=None):
+    """Dit::forward_batch on the fp16 path (engine/src/dit.cu:357-546, step cache at :404-433, :532-536): every batch
     item starts from the same latent [16, Hl, Wl]; outs: B latents [16, Hl, Wl] (the velocity predictions).
     ctx[b] = (prepared K/V of block i -> list over blocks, real rows, padding rows); nag as in block_forward16
     but with per-block prepared K/V lists."""
@@ -165,10 +177,35 @@ def forward16(outs, latent, t, sw, blocks, ws, B, rope, ctx, nag=None, eps=1e-6)
     linear_f32(X[:T], tok, sw.x_embed)
     for b in range(1, B):
         X[b * T:(b + 1) * T].copy_(X[:T])
+    use_cache = sc is not None and sc.threshold > 0
+    if use_cache:
+        R = B * T
+        if sc.R != R or sc.r0 is None:
+            sc.valid, sc.R = False, R
+            sc.r0 = torch.empty(R, D, device=dev)
+            sc.resid = torch.empty(R, D, device=dev)
+            sc.acc = torch.empty(2, device=dev)
+        X0 = X.clone()  # input of block 0
+        sc.skipped = False
     for i, blk in enumerate(blocks):
+        if use_cache and i == 1:
+            sub(X0, X, X0)  # block 0's residual of this step
+            if sc.valid:
+                rel_l1(X0, sc.r0, sc.acc)
+                h = sc.acc.cpu()  # synchronizes, as the reference's cudaMemcpy does
+                sc.last_change = float(h[0] / h[1]) if h[1] > 0 else 1.0
+                if sc.allow and sc.last_change < sc.threshold:
+                    add_gated(X, sc.resid)  # X = block-0 output + cached residual of blocks 1..N-1
+                    sc.skipped = True
+                    break
+            sc.r0.copy_(X0)
+            sc.resid.copy_(X)  # block-0 output, turned into the residual below
         cb = [(c[0][i], c[1], c[2]) for c in ctx]
         nb = None if nag is None else (nag[0][i],) + tuple(nag[1:])
         block_forward16(X, mods[i], blk, ws, B, T, rope, cb, nag=nb, eps=eps)
+    if use_cache and not sc.skipped:
+        sub(sc.resid, X, sc.resid)  # the residual of blocks 1..N-1
+        sc.valid = True
     N = torch.empty_like(X)
     layernorm_mod(N, X, fmod[D:2 * D], fmod[:D], eps)
     y = torch.empty(B * T, 64, device=dev)

@@ -26,10 +26,15 @@ def flow_sigmas(steps, shift=1.0, denoise=1.0):
     return s[len(s) - (steps + 1):]
 
 
-def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=1.0, init=None, negative=True):
+def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=1.0, init=None, negative=True,
+                 cache=None, cache_start=0.15, cache_end=0.9, cache_max_hits=2):
     """model(outs, x, t, cfg_now) writes the velocity of the prompt into outs[0] and, when cfg_now, of the
     negative context into outs[1]; x [16, Hl, Wl] fp32 (overwritten with the result), noise like x;
-    negative: whether a negative context exists (CFG runs for the first ceil(cfg_until * steps) steps)."""
+    negative: whether a negative context exists (CFG runs for the first ceil(cfg_until * steps) steps).
+    cache: a kiln_amd.dit.StepCache the model's forward uses, or None; the sampler allows a skip only after the
+    first max(2, ceil(cache_start * steps)) steps, before the last max(1, ceil((1 - cache_end) * steps)), and
+    for at most cache_max_hits steps in a row (engine/src/pipeline.cu:463-480, 488, 506-509). Returns x; the
+    number of skipped steps is in cache.skips."""
     import torch
     steps = len(sigmas) - 1
     if steps < 1:
@@ -38,11 +43,25 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
         return x
     v, vn = torch.empty_like(x), torch.empty_like(x)
     cfg_steps = math.ceil(cfg_until * steps - 1e-4) if negative else 0
+    warm = max(2, math.ceil(cache_start * steps))
+    tail = max(1, math.ceil((1.0 - cache_end) * steps))
+    max_hits = steps if cache_max_hits < 0 else cache_max_hits
+    run = 0
+    if cache is not None:
+        cache.skips = 0
     flow_start(x, noise, sigmas[0], init)
     for i in range(steps):
         s = sigmas[i]
         cfg_now = i < cfg_steps
+        if cache is not None:
+            cache.allow = warm <= i < steps - tail and run < max_hits
         model([v, vn], x, s * timestep_mult, cfg_now)
+        if cache is not None:
+            if cache.skipped:
+                cache.skips += 1
+                run += 1
+            else:
+                run = 0
         if cfg_now:
             cfg_combine(v, vn, cfg)
         flow_euler_step(x, v, s, sigmas[i + 1])

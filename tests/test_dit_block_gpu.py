@@ -237,3 +237,48 @@ def test_matvec_bf16_grouped(gpu):
         ref = oracle.matvec_bf16(Wb[i], x[i].numpy(), add.numpy())
         bar = np.sqrt(cols) * 2.0 ** -21 * (np.abs(W[i].float().numpy()) @ np.abs(x[i].numpy())) + 1e-6
         assert (np.abs(y[i].cpu().numpy() - ref) <= bar).all()
+
+
+def test_step_cache_skip_reuses_residual(gpu):
+    """First-block step cache (engine/src/dit.cu:404-433, 532-536): a second forward whose block-0 residual did
+    not move skips blocks 1..N-1 and returns the same latents (block-0 output + the cached residual); with
+    allow off it runs in full; the relative-L1 and difference kernels against numpy."""
+    g = torch.Generator().manual_seed(33)
+    blocks = []
+    for _ in range(3):
+        _, blk = _make_block(g)
+        blk.mod = [_bf16w(g, 256, D).to(DEV), _bf16w(g, 3 * D, 256).to(DEV)] * 3
+        blocks.append(blk)
+    sw = dit.StepWeights(_bf16w(g, D, D).to(DEV), _bf16w(g, 3 * D, D).to(DEV), _bf16(torch.ones(D)).to(DEV),
+                         _bf16w(g, 256, D).to(DEV), _bf16w(g, 2 * D, 256).to(DEV), _bf16w(g, D, 68).to(DEV),
+                         _bf16w(g, 64, D).to(DEV))
+    ctxs = [torch.randn(r, DCTX, generator=g).to(DEV) for r in REALS]
+    kv = [[blk.prepare_context(c, EPS) for blk in blocks] for c in ctxs]
+    rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
+    ws = dit.Workspace(B, T, D, F, DEV)
+    latent = torch.randn(16, 2 * Hp, 2 * Wp, generator=g).to(DEV)
+    args = (0.4, sw, blocks, ws, B, (rc.to(DEV), rs.to(DEV)), [(kv[i], REALS[i], L - REALS[i]) for i in range(B)])
+    sc = dit.StepCache(0.05)
+    sc.allow = True
+    o1 = [torch.empty_like(latent) for _ in range(B)]
+    dit.forward16(o1, latent, *args, sc=sc)
+    assert not sc.skipped and sc.valid
+    o2 = [torch.empty_like(latent) for _ in range(B)]
+    dit.forward16(o2, latent, *args, sc=sc)
+    assert sc.skipped and sc.last_change == 0.0
+    for a, b in zip(o1, o2):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+    sc.allow = False
+    o3 = [torch.empty_like(latent) for _ in range(B)]
+    dit.forward16(o3, latent, *args, sc=sc)
+    assert not sc.skipped
+    for a, b in zip(o1, o3):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+    a, b = torch.randn(100003, generator=g), torch.randn(100003, generator=g)
+    acc = torch.empty(2, device=DEV)
+    kiln_amd.rel_l1(a.to(DEV), b.to(DEV), acc)
+    ref = [np.abs(a.double().numpy() - b.double().numpy()).sum(), np.abs(b.double().numpy()).sum()]
+    np.testing.assert_allclose(acc.cpu().double().numpy(), ref, rtol=1e-5)
+    y = torch.empty(100003, device=DEV)
+    kiln_amd.sub(y, a.to(DEV), b.to(DEV))
+    np.testing.assert_array_equal(y.cpu().numpy(), (a - b).numpy())

@@ -59,3 +59,30 @@ def test_flow_kernels_and_euler_cfg_loop(gpu):
         xr = xr + vp * (sig[i + 1] - sig[i])
     assert calls == [(round(s * 1000.0, 6), i < 2) for i, s in enumerate(sig[:-1])]
     np.testing.assert_allclose(xg.cpu().numpy(), xr, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.gpu
+def test_step_cache_guards(gpu):
+    """The sampler's cache guards (engine/src/pipeline.cu:463-480): no skip before max(2, ceil(0.15 steps)), none
+    in the last max(1, ceil(0.1 steps)) steps, at most cache_max_hits in a row. A stub model records `allow` and
+    skips whenever allowed."""
+    from kiln_amd import dit
+
+    class Stub:
+        def __init__(self, cache):
+            self.cache, self.allowed = cache, []
+
+        def __call__(self, outs, xx, t, cfg_now):
+            self.allowed.append(self.cache.allow)
+            self.cache.skipped = self.cache.allow
+            outs[0].zero_()
+
+    sc = dit.StepCache(0.1)
+    stub = Stub(sc)
+    x = torch.empty(16, 4, 4, device=DEV)
+    sampler.sample_euler(stub, x, torch.zeros(16, 4, 4, device=DEV), sampler.flow_sigmas(20, 3.0), negative=False,
+                         cache=sc)
+    # steps 0-2 warm (ceil(0.15 * 20) = 3), last 2 (ceil(0.1 * 20)) off, then 2 skips and one full step repeating
+    expect = [False] * 3 + [True, True, False] * 5
+    expect = (expect + [False] * 20)[:18] + [False, False]
+    assert stub.allowed == expect and sc.skips == sum(expect)

@@ -226,6 +226,19 @@ int kiln_dit_self_attn_fused(void* out, int out_dtype, int ldo, const void* q, c
  * workspace that still holds the prepared K/V runs the same call unsplit. */
 size_t kiln_dit_self_attn_workspace_bytes(int B, int T, int H);
 
+/* The DiT self-attention section from the block's fp16 LayerNorm output (engine/src/dit.cu:460-469: linear16 of
+ * sa_q, sa_k, sa_v, rmsnorm of Q and K per head, rope_half, attention16 per item) in two launches: one fp16 GEMM
+ * of x16 [B*T, D] (D = 128 H) with the stacked [Wq; Wk; Wv] weight (kiln_linear16_prepare_weight of [3D, D])
+ * whose epilogue applies the QK-RMSNorm (bf16 weights) and RoPE (tables [T, 64]) and writes fp16 Q and the
+ * prepared K/V (no fp32 Q/K/V round trip, no K/V prepare pass), then the attention of the B items. H even,
+ * B <= 4. workspace: kiln_dit_self_attn_x16_workspace_bytes (fp16 Q, prepared K/V, key-split partials),
+ * 16-byte aligned (KILN_ENOMEM if smaller). out [B*T, ldo] fp32 or fp16. */
+int kiln_dit_self_attn_x16(void* out, int out_dtype, int ldo, const uint16_t* x16, const uint16_t* wqkv_prepped,
+                           const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps, const float* rope_cos,
+                           const float* rope_sin, int B, int T, int H, void* workspace, size_t ws_bytes,
+                           kiln_stream_t stream);
+size_t kiln_dit_self_attn_x16_workspace_bytes(int B, int T, int H);
+
 /* DiT cross-attention of a CFG batch plus NAG (engine/src/dit.cu:473-487): batch item b's queries
  * (rows b*T of q, RMS-normed inside with q_norm_w) attend to prepared context kvp[b] (Lk[b] real keys,
  * npad[b] zero keys). If kvp_neg is not NULL, item 0's queries also attend to kvp_neg into

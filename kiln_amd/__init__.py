@@ -64,6 +64,8 @@ _SIGS = {
     "kiln_dit_self_attn_fused": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp,
                                       _sz, _vp]),
     "kiln_dit_self_attn_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kiln_dit_self_attn_x16": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "kiln_dit_self_attn_x16_workspace_bytes": (_sz, [_i, _i, _i]),
     "kiln_cross_attn_nag": (_i, [_vp, _vp, _i, _i, _vp, _i, _i, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _f,
                                  _f, _f, _vp]),
 }
@@ -402,3 +404,17 @@ def rel_l1(a, b, acc, stream=None):
     """k_rel_l1 (engine/src/dit.cu:327-335): acc[0] = sum|a - b|, acc[1] = sum|b| (device float[2])."""
     _check(lib().kiln_rel_l1(_ptr(a), _ptr(b), a.numel(), _ptr(acc), _stream(stream)))
     return acc
+
+
+def dit_self_attn_x16(out, x16, wqkv, B, T, H, q_norm_w, k_norm_w, rope, eps=1e-6, workspace=None, stream=None):
+    """The DiT self-attention section from the fp16 LayerNorm output: QKV projection (wqkv: a PreppedWeight of
+    [3D, D]) with QK-norm + RoPE + K/V preparation fused into its epilogue, then attention (kiln_dit_self_attn_x16)."""
+    import torch
+    if workspace is None:
+        workspace = torch.empty(lib().kiln_dit_self_attn_x16_workspace_bytes(B, T, H), dtype=torch.uint8,
+                                device=x16.device)
+    rc, rs = rope
+    _check(lib().kiln_dit_self_attn_x16(_ptr(out), _dt(out), _ld(out), _ptr(x16), _ptr(wqkv.buf),
+                                        _bf16_bits(q_norm_w), _bf16_bits(k_norm_w), eps, _ptr(rc), _ptr(rs), B, T, H,
+                                        _ptr(workspace), workspace.numel(), _stream(stream)))
+    return out

@@ -814,7 +814,7 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
     p.store_pairs = pairs;
     p.qw = a.qw;
     p.eps = a.eps;
-    p.qscale = LOG2E / sqrtf((float)HD);
+    p.qscale = a.q_prescaled ? 1.0f : LOG2E / sqrtf((float)HD);
     p.rcos = a.rcos;
     p.rsin = a.rsin;
     p.ksplit = a.part && a.ksplit > 1 ? a.ksplit : 1;

@@ -350,6 +350,80 @@ int kiln_dit_self_attn_fused(void* out, int out_dtype, int ldo, const void* q, c
                       rope_cos, rope_sin, workspace, ws_bytes, (hipStream_t)stream);
 }
 
+static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+size_t kiln_dit_self_attn_x16_workspace_bytes(int B, int T, int H) {
+    if (B <= 0 || T <= 0 || H <= 0) return 0;
+    const size_t q = align256((size_t)B * T * H * kiln::HD * 2), kv = align256(kiln_kv_prepped_bytes(T, H));
+    const int ks = kiln::attn_key_split(B, T, T, H);
+    return q + kv * B + kiln::attn_split_bytes(ks, B, T, H);
+}
+
+int kiln_dit_self_attn_x16(void* out, int out_dtype, int ldo, const uint16_t* x16, const uint16_t* wqkv_prepped,
+                           const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps, const float* rope_cos,
+                           const float* rope_sin, int B, int T, int H, void* workspace, size_t ws_bytes,
+                           kiln_stream_t stream) {
+    if (out_dtype != KILN_F32 && out_dtype != KILN_F16) return fail(KILN_EINVAL, "dtype");
+    if (B <= 0 || T <= 0 || H <= 0) return fail(KILN_EINVAL, "bad sizes B=%d T=%d H=%d", B, T, H);
+    if (B > kiln::MAX_JOBS || H % 2 || T > MAX_TK)
+        return fail(KILN_EUNSUPPORTED, "dit_self_attn_x16: needs B <= %d, an even H and T <= %d (B=%d H=%d T=%d)",
+                    kiln::MAX_JOBS, MAX_TK, B, H, T);
+    if (!out || !x16 || !wqkv_prepped || !q_norm_w || !k_norm_w || !rope_cos || !rope_sin || !workspace)
+        return fail(KILN_EINVAL, "null pointer");
+    if (!aligned16(x16) || !aligned16(wqkv_prepped) || !aligned16(rope_cos) || !aligned16(rope_sin) ||
+        !aligned16(workspace) || ldo % 2)
+        return fail(KILN_EUNSUPPORTED, "operands not 16-byte aligned / ldo odd");
+    if (ws_bytes < kiln_dit_self_attn_x16_workspace_bytes(B, T, H))
+        return fail(KILN_ENOMEM, "workspace %zu bytes < %zu", ws_bytes, kiln_dit_self_attn_x16_workspace_bytes(B, T, H));
+    const int D = H * kiln::HD;
+    char* ws = static_cast<char*>(workspace);
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(ws);
+    ws += align256((size_t)B * T * D * 2);
+    const size_t kvb = align256(kiln_kv_prepped_bytes(T, H));
+    uint16_t* kvp[kiln::MAX_JOBS] = {};
+    for (int b = 0; b < B; b++) kvp[b] = reinterpret_cast<uint16_t*>(ws + kvb * b);
+    float* part = reinterpret_cast<float*>(ws + kvb * B);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = hip_check(kiln::launch_kv_zero_tail(kvp, B, T, H, s), "kv tail launch");
+    if (rc) return rc;
+    kiln::GemmLaunch g{};
+    g.a = x16;
+    g.w = wqkv_prepped;
+    g.K = D;
+    g.M = B * T;
+    g.N = 3 * D;
+    g.c = nullptr;
+    g.ldc = 3 * D;
+    g.epi = 4;
+    g.wprep = true;
+    g.q16 = q16;
+    for (int b = 0; b < B; b++) g.kvp[b] = kvp[b];
+    g.T = T;
+    g.H = H;
+    g.qw = q_norm_w;
+    g.kw = k_norm_w;
+    g.eps = eps;
+    g.rcos = rope_cos;
+    g.rsin = rope_sin;
+    rc = hip_check(kiln::launch_gemm16(g, s), "qkv projection launch");
+    if (rc) return rc;
+    const DT od = (DT)out_dtype;
+    const size_t osz = od == DT::F16 ? 2 : 4;
+    kiln::AttnLaunch a{};
+    for (int b = 0; b < B; b++) a.job[b] = {q16 + (size_t)b * T * D, kvp[b], (char*)out + (size_t)b * T * ldo * osz, T, 0};
+    a.njobs = B;
+    a.Tq = T;
+    a.H = H;
+    a.ldq = D;
+    a.ldo = ldo;
+    a.in = DT::F16;
+    a.out = od;
+    a.q_prescaled = true;
+    a.ksplit = kiln::attn_key_split(B, T, T, H);
+    a.part = a.ksplit > 1 ? part : nullptr;
+    return hip_check(kiln::launch_attn_fwd(a, s), "attn_fwd launch");
+}
+
 int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
                         const uint16_t* q_norm_w, float eps, int B, int T, int H, const uint16_t* const* kvp,
                         const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,

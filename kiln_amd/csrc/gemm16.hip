@@ -80,12 +80,135 @@ struct GemmParams {
     int tiles_m, tiles_n, total, per;
     int pairs;  // output rows or base not 16-byte (fp32) / 8-byte (fp16) aligned: store element pairs
     int wprep;  // w is in the prepared tile layout (kiln_linear16_prepare_weight), not [N, K] rows
+    // EPI_QKV (the DiT self-attention projection with its QK-RMSNorm, RoPE and fp16 K/V preparation fused):
+    // columns [0, D) are Q, [D, 2D) K, [2D, 3D) V of H heads; row r is token r % T of item r / T
+    _Float16* q16;      // [M, D]: fp16(rope(rmsnorm(q)) * qscale)
+    uint16_t* kvp[MAX_JOBS];  // prepared K/V per item (common.hpp layout), K = rope(rmsnorm(k))
+    int T, H;
+    const uint16_t* qw;  // bf16 [128] norm weights
+    const uint16_t* kw;
+    float eps, qscale;
+    const float* rcos;  // [T, 64]
+    const float* rsin;
+};
+constexpr int EPI_QKV = 4;
+struct KvTailJobs {
+    uint16_t* kvp[MAX_JOBS];
 };
 
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.f + erff(v * 0.70710678118654752f)); }
+
+// EPI_QKV epilogue. The workgroup's 256 columns are two heads of one region (Q, K or V: D is a multiple of 256).
+// A wave holds 64 columns = half a head; its partner wave (wv ^ 2, the same rows) holds the other half. Q/K:
+// per-row sum of squares over the head (own half + partner's, through LDS), scale by rsqrt(mean + eps) and the
+// bf16 weight, then RoPE, whose pairs (i, i + 64) are the same accumulator element of the two partner waves
+// (exchanged through LDS two row blocks at a time). Q is stored as fp16(q * qscale) rows, K and V in the
+// prepared K/V layout of their item (kv_k_off / kv_v_off).
+template <int MB>
+__device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)[NBW][MB], _Float16* lds, int m0,
+                                             int n0, int wv, int wn, int wm, int lane) {
+    const int D = p.H * HD;
+    const int region = n0 / D, c0 = n0 - region * D;
+    const int hd = (c0 + wn * 64) / HD, half = wn & 1;
+    const int rl = lane & 15, cq = 4 * (lane >> 4);  // column within the wave's 64: nb*16 + cq + e
+    const int rbase = m0 + wm * 16 * MB + rl;
+    float* lf = reinterpret_cast<float*>(lds);
+    __syncthreads();  // every wave is done with the k loop's LDS stages
+    if (region < 2) {
+        const uint16_t* w = region == 0 ? p.qw : p.kw;
+        float r[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            float ss = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) ss += acc[nb][mb][e] * acc[nb][mb][e];
+            ss += __shfl_xor(ss, 16, 64);
+            ss += __shfl_xor(ss, 32, 64);
+            if (lane < 16) lf[wv * 16 * MB + mb * 16 + rl] = ss;
+            r[mb] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) r[mb] = rsqrtf((r[mb] + lf[(wv ^ 2) * 16 * MB + mb * 16 + rl]) * (1.0f / HD) + p.eps);
+        float wt[NBW][4];
+#pragma unroll
+        for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) wt[nb][e] = bf16_to_f32(w[half * 64 + nb * 16 + cq + e]);
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[nb][mb][e] *= r[mb] * wt[nb][e];
+        // RoPE partner exchange, two row blocks per round: [wave][mb in round][nb][lane][e]
+        constexpr int XW = 2 * NBW * 64 * 4;  // floats per wave per round
+#pragma unroll
+        for (int g0 = 0; g0 < MB; g0 += 2) {
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                if (g0 + j < MB)
+#pragma unroll
+                    for (int nb = 0; nb < NBW; nb++)
+                        *reinterpret_cast<floatx4*>(lf + wv * XW + ((j * NBW + nb) * 64 + lane) * 4) = acc[nb][g0 + j];
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                if (g0 + j >= MB) continue;
+                const int row = rbase + (g0 + j) * 16;
+                const int t = (row < p.M ? row : 0) % p.T;
+#pragma unroll
+                for (int nb = 0; nb < NBW; nb++) {
+                    const floatx4 o = *reinterpret_cast<const floatx4*>(lf + (wv ^ 2) * XW + ((j * NBW + nb) * 64 + lane) * 4);
+                    const floatx4 cs = *reinterpret_cast<const floatx4*>(p.rcos + (size_t)t * 64 + nb * 16 + cq);
+                    const floatx4 sn = *reinterpret_cast<const floatx4*>(p.rsin + (size_t)t * 64 + nb * 16 + cq);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float v = acc[nb][g0 + j][e];
+                        acc[nb][g0 + j][e] = half == 0 ? v * cs[e] - o[e] * sn[e] : v * cs[e] + o[e] * sn[e];
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const int row = rbase + mb * 16;
+        if (row >= p.M) continue;
+        const int b = row / p.T, key = row - b * p.T;
+        _Float16* kv = reinterpret_cast<_Float16*>(p.kvp[b]) + (size_t)hd * kv_head_stride(p.T) +
+                       (size_t)(key / KT) * KV_TILE_H;
+        const int kc = (key % KT) / 32, k32 = key % 32;
+#pragma unroll
+        for (int nb = 0; nb < NBW; nb++) {
+            const int d = half * 64 + nb * 16 + cq;  // 4 consecutive d, inside one 8-element chunk
+            const floatx4 v = acc[nb][mb];
+            if (region == 0) {
+                *reinterpret_cast<half4*>(p.q16 + (size_t)row * D + hd * HD + d) =
+                    half4{(_Float16)(v[0] * p.qscale), (_Float16)(v[1] * p.qscale), (_Float16)(v[2] * p.qscale),
+                          (_Float16)(v[3] * p.qscale)};
+            } else if (region == 1) {
+                const int klane = k32 + 32 * ((d % 16) / 8);
+                *reinterpret_cast<half4*>(kv + kv_k_off(kc, d / 16, klane) + d % 8) =
+                    half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            } else {
+                // V_c [t][db][lane][j]: d = 32 db + lane % 32, key = 16 t + 8 (j / 4) + 4 (lane / 32) + j % 4
+                const int tt = k32 / 16, jj = 4 * ((k32 / 8) % 2) + k32 % 4, lh = (k32 / 4) % 2;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int dd = d + e;
+                    kv[kv_v_off(kc, tt, dd / 32, dd % 32 + 32 * lh) + jj] = (_Float16)v[e];
+                }
+            }
+        }
+    }
+}
 
 template <int EPI, int MB>
 __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
@@ -252,6 +375,10 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
     }
     if (kt < KTT) step(False{}, kt, fw, gw);
 
+    if constexpr (EPI == EPI_QKV) {
+        qkv_epilogue<MB>(p, acc, lds, m0, n0, wv, wn, wm, lane);
+        return;
+    }
     // epilogue: lane holds rows m0 + wm*16*MB + mb*16 + (lane & 15), columns n0 + wn*64 + nb*16 + 4*(lane >> 4) + e
     const int mrow = m0 + wm * 16 * MB + rl;
     const int ncol = n0 + wn * NBW * 16 + 4 * (lane >> 4);
@@ -362,6 +489,21 @@ hipError_t launch_gemm_wprep(uint16_t* wp, const uint16_t* w, int N, int K, bool
     return hipGetLastError();
 }
 
+__global__ void k_kv_zero_tail(KvTailJobs j, size_t head_stride, size_t tail_off) {
+    // block (item, head): 32 KB of the last tile, 16 bytes per thread and step
+    _Float16* base = reinterpret_cast<_Float16*>(j.kvp[blockIdx.y]) + blockIdx.x * head_stride + tail_off;
+    for (int i = threadIdx.x; i < KV_TILE_H / 8; i += blockDim.x) reinterpret_cast<half8*>(base)[i] = half8{};
+}
+
+hipError_t launch_kv_zero_tail(uint16_t* const* kvp, int njobs, int T, int H, hipStream_t s) {
+    if (T % KT == 0 || njobs <= 0) return hipSuccess;
+    KvTailJobs j{};
+    for (int b = 0; b < njobs && b < MAX_JOBS; b++) j.kvp[b] = kvp[b];
+    hipLaunchKernelGGL(k_kv_zero_tail, dim3(H, njobs), dim3(256), 0, s, j, kv_head_stride(T),
+                       (size_t)(kv_tiles(T) - 1) * KV_TILE_H);
+    return hipGetLastError();
+}
+
 static int cu_count() {
     static int cus[64] = {};
     int dev = 0;
@@ -386,6 +528,7 @@ static hipError_t launch_mb(GemmParams p, int epi, hipStream_t s) {
         case KILN_EPI_F16: kern = k_gemm16<KILN_EPI_F16, MB>; break;
         case KILN_EPI_GELU16: kern = k_gemm16<KILN_EPI_GELU16, MB>; break;
         case KILN_EPI_RESID: kern = k_gemm16<KILN_EPI_RESID, MB>; break;
+        case EPI_QKV: kern = k_gemm16<EPI_QKV, MB>; break;
         default: return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(kern, dim3(nb), dim3(GTHR), lds, s, p);
@@ -428,6 +571,18 @@ hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s) {
     const size_t esz = (g.epi == KILN_EPI_F32 || g.epi == KILN_EPI_RESID) ? 4 : 2;
     p.pairs = ((size_t)g.c % (4 * esz) != 0) || (g.ldc % 4 != 0);
     p.wprep = g.wprep ? 1 : 0;
+    if (g.epi == EPI_QKV) {
+        p.q16 = reinterpret_cast<_Float16*>(g.q16);
+        for (int b = 0; b < MAX_JOBS; b++) p.kvp[b] = g.kvp[b];
+        p.T = g.T;
+        p.H = g.H;
+        p.qw = g.qw;
+        p.kw = g.kw;
+        p.eps = g.eps;
+        p.qscale = LOG2E / sqrtf((float)HD);
+        p.rcos = g.rcos;
+        p.rsin = g.rsin;
+    }
     if (gemm16_mb(g.M, g.N) == 7) return launch_mb<7>(p, g.epi, s);
     return launch_mb<8>(p, g.epi, s);
 }

@@ -31,6 +31,7 @@ struct AttnLaunch {
     const float* rsin;
     int ksplit;          // > 1: split every unit's keys into ksplit ranges (partials in `part`, then a merge)
     float* part;         // attn_split_bytes(ksplit, njobs, Tq, H) bytes of device scratch
+    bool q_prescaled;    // fp16 Q already holds q * log2(e)/sqrt(128) (no norm, no RoPE): scale 1
 };
 
 // Key ranges per unit for a launch of njobs x H heads x Tq queries against Tk keys: > 1 only when the grid
@@ -69,7 +70,18 @@ struct GemmLaunch {
     int M, N;
     int epi;
     bool wprep;  // w in the prepared layout of launch_gemm_wprep
+    // epi == 4 (the DiT self-attention projection, N = 3 * 128 * H, H even): Q rows and prepared K/V per item
+    uint16_t* q16;
+    uint16_t* kvp[MAX_JOBS];
+    int T, H;
+    const uint16_t* qw;
+    const uint16_t* kw;
+    float eps;
+    const float* rcos;
+    const float* rsin;
 };
+// zero the last (partial) 64-key tile of each item's and head's prepared K/V before a projection writes the keys
+hipError_t launch_kv_zero_tail(uint16_t* const* kvp, int njobs, int T, int H, hipStream_t s);
 hipError_t launch_gemm16(const GemmLaunch& g, hipStream_t s);
 // Weight [N, K] (fp16, or bf16 converted as the reference's weight_to_f16) into the prepared tile layout.
 size_t gemm16_prepped_bytes(int N, int K);

@@ -3,8 +3,9 @@
 Mirrors the block loop of the reference's Dit::forward_batch for G.fp16 && G.tc16 (engine/src/dit.cu:455-494):
 
     N16 = layernorm_mod16(X; shift, scale of the self-attention modulation)
-    Q, K, V = linear16(N16, sa_q / sa_k / sa_v)                         fp32 (one launch on [Wq; Wk; Wv])
-    A16 = attention16(rmsnorm+rope(Q), rmsnorm+rope(K), V) per item      kiln_dit_self_attn_fused, one launch
+    Q, K, V = linear16(N16, sa_q / sa_k / sa_v)   one launch on [Wq; Wk; Wv] whose epilogue applies
+    A16 = attention16(rmsnorm+rope(Q), ...)       QK-RMSNorm + RoPE and writes fp16 Q / prepared K/V,
+                                                  then one attention launch (kiln_dit_self_attn_x16)
     X += gate * linear16(A16, sa_o)                                      RESID epilogue
     N16 = layernorm_mod16(X; cross-attention modulation)
     Q = linear16(N16, ca_q)                                              fp32
@@ -22,9 +23,9 @@ Every call below goes to the HIP library; there is no CPU path.
 import numpy as np
 import torch
 
-from . import (KILN_EPI_F32, KILN_EPI_GELU16, KILN_EPI_RESID, cross_attn_nag, dit_self_attn,
-               dit_self_attn_workspace_bytes, kv_prepare, layernorm_mod, linear16, linear16_prepare_weight,
-               add_gated, linear_f32, matvec, matvec_grouped, patchify, rel_l1, rmsnorm, silu, sub, unpatchify)
+from . import (KILN_EPI_F32, KILN_EPI_GELU16, KILN_EPI_RESID, add_gated, cross_attn_nag, dit_self_attn_x16,
+               kv_prepare, layernorm_mod, lib, linear16, linear16_prepare_weight, linear_f32, matvec, matvec_grouped,
+               patchify, rel_l1, rmsnorm, silu, sub, unpatchify)
 
 HD = 128
 
@@ -62,11 +63,12 @@ class Workspace:
     def __init__(self, B, T, D, F, device):
         R = B * T
         self.n16 = torch.empty(R, D, dtype=torch.float16, device=device)
-        self.qkv = torch.empty(R, 3 * D, dtype=torch.float32, device=device)
+        self.q = torch.empty(R, D, dtype=torch.float32, device=device)
         self.a16 = torch.empty(R, D, dtype=torch.float16, device=device)
         self.an16 = torch.empty(T, D, dtype=torch.float16, device=device)
         self.h16 = torch.empty(R, F, dtype=torch.float16, device=device)
-        self.attn_ws = torch.empty(dit_self_attn_workspace_bytes(B, T, D // HD), dtype=torch.uint8, device=device)
+        self.attn_ws = torch.empty(lib().kiln_dit_self_attn_x16_workspace_bytes(B, T, D // HD), dtype=torch.uint8,
+                                   device=device)
 
 
 def block_forward16(X, mods, blk, ws, B, T, rope, ctx, nag=None, eps=1e-6):
@@ -75,11 +77,11 @@ def block_forward16(X, mods, blk, ws, B, T, rope, ctx, nag=None, eps=1e-6):
     tau, alpha) for item 0."""
     D, H = blk.D, blk.D // HD
     mo, mc, mm = mods[0:3 * D], mods[3 * D:6 * D], mods[6 * D:9 * D]
-    q, k, v = ws.qkv[:, 0:D], ws.qkv[:, D:2 * D], ws.qkv[:, 2 * D:3 * D]
-    # self-attention
+    q = ws.q
+    # self-attention: the Q/K/V projection's epilogue applies the QK-RMSNorm and RoPE and writes fp16 Q and the
+    # prepared K/V, then the attention of the B items (kiln_dit_self_attn_x16)
     layernorm_mod(ws.n16, X, mo[D:2 * D], mo[0:D], eps)
-    linear16(ws.qkv, ws.n16, blk.sa_qkv, epi=KILN_EPI_F32)
-    dit_self_attn(ws.a16, q, k, v, B, T, H, blk.sa_qn, blk.sa_kn, rope, eps=eps, workspace=ws.attn_ws)
+    dit_self_attn_x16(ws.a16, ws.n16, blk.sa_qkv, B, T, H, blk.sa_qn, blk.sa_kn, rope, eps=eps, workspace=ws.attn_ws)
     linear16(X, ws.a16, blk.sa_o, epi=KILN_EPI_RESID, gate=mo[2 * D:3 * D])
     # cross-attention, each item against its own context (+ NAG on item 0)
     layernorm_mod(ws.n16, X, mc[D:2 * D], mc[0:D], eps)

@@ -282,3 +282,41 @@ def test_step_cache_skip_reuses_residual(gpu):
     y = torch.empty(100003, device=DEV)
     kiln_amd.sub(y, a.to(DEV), b.to(DEV))
     np.testing.assert_array_equal(y.cpu().numpy(), (a - b).numpy())
+
+
+@pytest.mark.parametrize("Hh,Hp_,Wp_,Bb", [(4, 8, 12, 2), (2, 10, 10, 3), (16, 48, 72, 2)])
+def test_dit_self_attn_x16_fused_projection(gpu, Hh, Hp_, Wp_, Bb):
+    """kiln_dit_self_attn_x16 (QKV GEMM whose epilogue does QK-RMSNorm, RoPE and the K/V preparation) against
+    the float64 statement of dit.cu:460-469 on sampled rows (BASELINE bar: max-abs 2e-3, mean-abs 2e-4), and
+    against the unfused path (linear16 F32 + kiln_dit_self_attn_fused) on every output. T = 100 has a partial
+    last key tile; T = 3456 x 16 heads is config 5's shape."""
+    Dd, Tt = Hh * HD, Hp_ * Wp_
+    g = torch.Generator().manual_seed(34 + Hh)
+    x = (torch.randn(Bb * Tt, Dd, generator=g)).half()
+    wqkv = (torch.randn(3 * Dd, Dd, generator=g) * Dd ** -0.5).half()
+    qn, kn = (_bf16(1 + 0.2 * torch.randn(HD, generator=g)) for _ in range(2))
+    rc, rs = kiln_amd.cosmos_rope_tables(Hp_, Wp_)
+    rope = (rc.to(DEV), rs.to(DEV))
+    wp = kiln_amd.linear16_prepare_weight(wqkv.to(DEV))
+    out = torch.empty(Bb * Tt, Dd, dtype=torch.float16, device=DEV)
+    kiln_amd.dit_self_attn_x16(out, x.to(DEV), wp, Bb, Tt, Hh, qn.to(DEV), kn.to(DEV), rope)
+    qkv = torch.empty(Bb * Tt, 3 * Dd, device=DEV)
+    kiln_amd.linear16(qkv, x.to(DEV), wp)
+    ref_u = torch.empty_like(out)
+    kiln_amd.dit_self_attn(ref_u, qkv[:, :Dd], qkv[:, Dd:2 * Dd], qkv[:, 2 * Dd:], Bb, Tt, Hh, qn.to(DEV), kn.to(DEV),
+                           rope)
+    torch.cuda.synchronize()
+    du = (out.float() - ref_u.float()).abs()
+    assert du.max().item() <= 2e-3 and du.mean().item() <= 1e-4, (du.max().item(), du.mean().item())
+    # float64 statement on sampled query rows of every item
+    qkv64 = x.double() @ wqkv.double().T
+    sel = torch.randperm(Tt, generator=g)[:64]
+    errs = []
+    for b in range(Bb):
+        rows = slice(b * Tt, (b + 1) * Tt)
+        q = _rope(_rms(qkv64[rows, :Dd], qn.float().double(), Hh, EPS), rc.double(), rs.double(), Hh)
+        k = _rope(_rms(qkv64[rows, Dd:2 * Dd], kn.float().double(), Hh, EPS), rc.double(), rs.double(), Hh)
+        ref = _attn(q[sel], k, qkv64[rows, 2 * Dd:], Hh)
+        errs.append((out[b * Tt:(b + 1) * Tt][sel.to(DEV)].cpu().double() - ref).abs())
+    e = torch.cat(errs)
+    assert e.max().item() <= 2e-3 and e.mean().item() <= 2e-4, (e.max().item(), e.mean().item())

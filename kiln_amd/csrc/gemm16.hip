@@ -99,7 +99,27 @@ struct KvTailJobs {
 __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.f + erff(v * 0.70710678118654752f)); }
+// GELU(v) = v Phi(v) = v (1 + erf(v / sqrt 2)) / 2, with Phi from erfc, which keeps its relative accuracy in the
+// negative tail: Phi(v) = erfc(z) / 2 for v < 0 and 1 - erfc(z) / 2 for v >= 0, z = |v| / sqrt 2. erfc(z) for
+// z >= 0 is the Chebyshev approximation "erfcc" of Numerical Recipes in C (Press et al., 2nd ed., section 6.2),
+// fractional error below 1.2e-7 everywhere: ~17 VALU operations and no branches, about half of a library erff,
+// and far below the fp16 output's rounding.
+__device__ __forceinline__ float gelu_erf(float v) {
+    const float z = fabsf(v) * 0.70710678118654752f;
+    const float t = __builtin_amdgcn_rcpf(1.f + 0.5f * z);
+    float r = 0.17087277f;
+    r = fmaf(t, r, -0.82215223f);
+    r = fmaf(t, r, 1.48851587f);
+    r = fmaf(t, r, -1.13520398f);
+    r = fmaf(t, r, 0.27886807f);
+    r = fmaf(t, r, -0.18628806f);
+    r = fmaf(t, r, 0.09678418f);
+    r = fmaf(t, r, 0.37409196f);
+    r = fmaf(t, r, 1.00002368f);
+    r = fmaf(t, r, -1.26551223f);
+    const float half_erfc = 0.5f * t * __expf(r - z * z);
+    return v * (v >= 0.f ? 1.f - half_erfc : half_erfc);
+}
 
 // EPI_QKV epilogue. The workgroup's 256 columns are two heads of one region (Q, K or V: D is a multiple of 256).
 // A wave holds 64 columns = half a head; its partner wave (wv ^ 2, the same rows) holds the other half. Q/K:

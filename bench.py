@@ -414,6 +414,33 @@ def main():
 
     lin, blk_us, blk_fl = linear16_cases(torch, kiln_amd, tm, dev, args.steps, args.warmup)
 
+    # the self-attention section of one DiT block at config 5 from the fp16 LayerNorm output: fused (QKV GEMM
+    # epilogue does QK-norm + RoPE + K/V preparation, then attention) against unfused (fp32 QKV GEMM, then the
+    # fused attention call with its K/V prepare pass)
+    T5, D5 = 3456, H * D
+    g6 = torch.Generator(device=dev).manual_seed(66)
+    x16 = torch.randn(2 * T5, D5, generator=g6, device=dev).half()
+    wqkv = kiln_amd.linear16_prepare_weight(linear_init(torch, 3 * D5, D5, g6, dev).half())
+    nw5 = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    c5, s5 = kiln_amd.cosmos_rope_tables(48, 72)
+    rope5 = (c5.to(dev), s5.to(dev))
+    a5 = torch.empty(2 * T5, D5, dtype=torch.float16, device=dev)
+    ws5 = torch.empty(L.kiln_dit_self_attn_x16_workspace_bytes(2, T5, H), dtype=torch.uint8, device=dev)
+    qkv5 = torch.empty(2 * T5, 3 * D5, device=dev)
+    wsu = torch.empty(kiln_amd.dit_self_attn_workspace_bytes(2, T5, H), dtype=torch.uint8, device=dev)
+    ms_fz = tm.run(lambda: kiln_amd.dit_self_attn_x16(a5, x16, wqkv, 2, T5, H, nw5, nw5, rope5, workspace=ws5),
+                   args.steps, args.warmup)
+
+    def unfused():
+        kiln_amd.linear16(qkv5, x16, wqkv)
+        kiln_amd.dit_self_attn(a5, qkv5[:, :D5], qkv5[:, D5:2 * D5], qkv5[:, 2 * D5:], 2, T5, H, nw5, nw5, rope5,
+                               workspace=wsu)
+
+    ms_uf = tm.run(unfused, args.steps, args.warmup)
+    log(f"config 5 self-attention section from x16 (QKV GEMM + attention): fused epilogue {ms_fz * 1e3:.1f} us, "
+        f"unfused {ms_uf * 1e3:.1f} us")
+    del x16, wqkv, a5, ws5, qkv5, wsu
+
     cfgb = dit_forward_case(torch, kiln_amd, dev)
     ms_blk = tm.run(cfgb["step"], max(3, args.steps // 5), 1)
     log(f"config 5, DiT forward of the CFG pair on the fp16 path (step tables, embed, 28 blocks, final layer): "
@@ -475,6 +502,8 @@ def main():
             "linear16_torch_f16out_tflops": {k: round(v["torch_tflops"], 1) for k, v in lin.items()},
             "linear16_dit_block_us": round(blk_us, 1),
             "linear16_dit_block_tflops": round(blk_fl / blk_us / 1e6, 1),
+            "dit_self_attn_section_fused_us": round(ms_fz * 1e3, 1),
+            "dit_self_attn_section_unfused_us": round(ms_uf * 1e3, 1),
             "dit_forward_ms_per_step": round(ms_blk, 3),
             "dit_forward_tflops": round(cfgb_flop / ms_blk / 1e9, 1),
             "dit_sample_8_steps_ms": round(ms_s8, 1),

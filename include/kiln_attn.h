@@ -162,6 +162,10 @@ int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* 
  * the relative L1 change, acc[0] = sum |a - b|, acc[1] = sum |b| (device float[2], overwritten; k_rel_l1). */
 int kiln_sub(float* y, const float* a, const float* b, size_t n, kiln_stream_t stream);
 int kiln_rel_l1(const float* a, const float* b, size_t n, float* acc, kiln_stream_t stream);
+/* Replaces torch_randn() (engine/src/pipeline.cu:17-64): host memory out[n] = torch.manual_seed(seed);
+ * torch.randn(n) on the CPU (MT19937, 24-bit uniforms, Box-Muller in blocks of 16). n >= 16. Host code: no
+ * device, no stream. The sampler's initial noise (pipeline.cu:428-429). */
+int kiln_torch_randn(float* host_out, uint64_t seed, size_t n);
 /* Flow-matching sampler start (engine/src/pipeline.cu:304-307, k_start): x = sigma * noise + (1 - sigma) * init
  * (init NULL: 0), n elements. */
 int kiln_flow_start(float* x, const float* noise, const float* init, float sigma, size_t n, kiln_stream_t stream);

@@ -46,6 +46,7 @@ _SIGS = {
     "kiln_cfg_combine": (_i, [_vp, _vp, _f, _sz, _vp]),
     "kiln_sub": (_i, [_vp, _vp, _vp, _sz, _vp]),
     "kiln_rel_l1": (_i, [_vp, _vp, _sz, _vp, _vp]),
+    "kiln_torch_randn": (_i, [_vp, ctypes.c_uint64, _sz]),
     "kiln_flow_start": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
     "kiln_flow_euler_step": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
@@ -417,4 +418,13 @@ def dit_self_attn_x16(out, x16, wqkv, B, T, H, q_norm_w, k_norm_w, rope, eps=1e-
     _check(lib().kiln_dit_self_attn_x16(_ptr(out), _dt(out), _ld(out), _ptr(x16), _ptr(wqkv.buf),
                                         _bf16_bits(q_norm_w), _bf16_bits(k_norm_w), eps, _ptr(rc), _ptr(rs), B, T, H,
                                         _ptr(workspace), workspace.numel(), _stream(stream)))
+    return out
+
+
+def torch_randn(seed, n):
+    """torch_randn (engine/src/pipeline.cu:17-64): torch.manual_seed(seed); torch.randn(n) on the host, as a CPU
+    float32 tensor (the library's own MT19937 + Box-Muller)."""
+    import torch
+    out = torch.empty(n, dtype=torch.float32)
+    _check(lib().kiln_torch_randn(_ptr(out), seed, n))
     return out

@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkiln_attn.so")
-SOURCES = ["attn_fwd.hip", "elementwise.hip", "gemm16.hip", "dit_aux.hip", "capi.cpp"]
+SOURCES = ["attn_fwd.hip", "elementwise.hip", "gemm16.hip", "dit_aux.hip", "host_rng.cpp", "capi.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

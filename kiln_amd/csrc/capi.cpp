@@ -624,6 +624,12 @@ int kiln_rel_l1(const float* a, const float* b, size_t n, float* acc, kiln_strea
     return hip_check(kiln::launch_rel_l1(a, b, n, acc, (hipStream_t)stream), "rel_l1 launch");
 }
 
+int kiln_torch_randn(float* host_out, uint64_t seed, size_t n) {
+    if (!host_out) return fail(KILN_EINVAL, "torch_randn: null pointer");
+    if (!kiln::host_torch_randn(host_out, seed, n)) return fail(KILN_EUNSUPPORTED, "torch_randn: n=%zu < 16", n);
+    return KILN_OK;
+}
+
 int kiln_flow_start(float* x, const float* noise, const float* init, float sigma, size_t n, kiln_stream_t stream) {
     if (n && (!x || !noise)) return fail(KILN_EINVAL, "flow_start: null pointer");
     if (!n) return KILN_OK;

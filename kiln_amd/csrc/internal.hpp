@@ -103,6 +103,9 @@ hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, h
 hipError_t launch_flow_start(float* x, const float* noise, const float* init, float s, size_t n, hipStream_t st);
 hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st);
 
+// torch.manual_seed(seed); torch.randn(n) on the host (host_rng.cpp); false if n < 16
+bool host_torch_randn(float* out, uint64_t seed, size_t n);
+
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s);
 

@@ -26,6 +26,15 @@ def flow_sigmas(steps, shift=1.0, denoise=1.0):
     return s[len(s) - (steps + 1):]
 
 
+def initial_noise(seed, shape, device):
+    """The sampler's noise (engine/src/pipeline.cu:428-429): torch_randn(seed, n) on the host, then to the device."""
+    from . import torch_randn
+    n = 1
+    for d in shape:
+        n *= d
+    return torch_randn(seed, n).view(*shape).to(device)
+
+
 def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=1.0, init=None, negative=True,
                  cache=None, cache_start=0.15, cache_end=0.9, cache_max_hits=2):
     """model(outs, x, t, cfg_now) writes the velocity of the prompt into outs[0] and, when cfg_now, of the

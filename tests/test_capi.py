@@ -115,3 +115,17 @@ def test_cpp_host_header_compiles():
     r = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-fsyntax-only", "-x", "hip", "-", "-I", kiln_amd.os.path.dirname(kiln_amd._HERE)],
                        input=src, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+@pytest.mark.parametrize("seed", [0, 42, 123456789])
+def test_torch_randn_host_matches_torch_fixture(seed):
+    """kiln_torch_randn (the library's host torch_randn, engine/src/pipeline.cu:17-64) against the torch.randn bit
+    patterns committed in tests/golden (torch's vectorized log/cos differ from libm by a few ulp)."""
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", f"randn_seed{seed}.json")) as f:
+        fx = json.load(f)
+    ref = np.array([int(b, 16) for b in fx["bits"]], dtype=np.uint32).view(np.float32)
+    got = kiln_amd.torch_randn(seed, len(ref)).numpy()
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 4 and (ulp == 0).mean() > 0.7

@@ -299,6 +299,8 @@ def main():
                     help="run only the config-4 attention kernel loop (for rocprofv3 runs)")
     ap.add_argument("--linear16-only", action="store_true",
                     help="run only the DiT-shape linear16 cases (for rocprofv3 runs)")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="run only the config-5 DiT forward of the CFG pair (for rocprofv3 runs)")
     ap.add_argument("--probe", action="store_true",
                     help="only run the sustained matrix-core probe (kiln_amd/probe/mfma_mix) and print its JSON")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
@@ -334,6 +336,11 @@ def main():
 
     if args.linear16_only:
         linear16_cases(torch, kiln_amd, tm, dev, args.steps, args.warmup)
+        return 0
+    if args.forward_only:
+        cf = dit_forward_case(torch, kiln_amd, dev)
+        ms = tm.run(cf["step"], args.steps, args.warmup)
+        log(f"config 5 DiT forward of the CFG pair: {ms:.3f} ms")
         return 0
 
     cfg4 = self_attn_case(torch, kiln_amd, 64, 64, 2, 4, dev)

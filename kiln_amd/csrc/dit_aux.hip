@@ -74,45 +74,39 @@ __global__ void k_unpatchify(float* __restrict__ lat, const float* __restrict__ 
     lat[((size_t)c * Hl + yy) * Wl + xx] = tok[(size_t)t * ldt + f];
 }
 
-// y [T, rows] (row stride ldy) = x [T, cols] (row stride ldx) W^T: 64 x 64 output tiles, k in chunks of 32 through
-// LDS, each thread 4 x 4 outputs in fp32.
+// y [T, rows] (row stride ldy) = x [T, cols] (row stride ldx) W^T: 16 x 64 output tiles (enough workgroups for the
+// final layer's 64 output columns), k in chunks of 64 through LDS, each thread 4 outputs of one row in fp32.
 __global__ __launch_bounds__(256) void k_linear_f32(float* __restrict__ y, int ldy, const float* __restrict__ x,
                                                     int ldx, const uint16_t* __restrict__ W, int T, int rows, int cols) {
-    __shared__ float xs[32][65];
-    __shared__ float ws[32][65];
-    const int t0 = blockIdx.y * 64, n0 = blockIdx.x * 64, tid = threadIdx.x;
-    const int tr = (tid >> 4) * 4, tc = (tid & 15) * 4;
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < cols; k0 += 32) {
-        for (int e = tid; e < 64 * 32; e += 256) {
-            const int r = e >> 5, k = e & 31;
-            const int tt = t0 + r, nn = n0 + r, kk = k0 + k;
-            xs[k][r] = (tt < T && kk < cols) ? x[(size_t)tt * ldx + kk] : 0.f;
-            ws[k][r] = (nn < rows && kk < cols) ? bf16_to_f32(W[(size_t)nn * cols + kk]) : 0.f;
+    __shared__ float xs[16][65];
+    __shared__ float ws[64][65];
+    const int t0 = blockIdx.y * 16, n0 = blockIdx.x * 64, tid = threadIdx.x;
+    const int tr = tid >> 4, tc = (tid & 15) * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < cols; k0 += 64) {
+        for (int e = tid; e < 16 * 64; e += 256) {
+            const int r = e >> 6, k = e & 63, tt = t0 + r, kk = k0 + k;
+            xs[r][k] = (tt < T && kk < cols) ? x[(size_t)tt * ldx + kk] : 0.f;
+        }
+        for (int e = tid; e < 64 * 64; e += 256) {
+            const int r = e >> 6, k = e & 63, nn = n0 + r, kk = k0 + k;
+            ws[r][k] = (nn < rows && kk < cols) ? bf16_to_f32(W[(size_t)nn * cols + kk]) : 0.f;
         }
         __syncthreads();
 #pragma unroll 8
-        for (int k = 0; k < 32; k++) {
-            float a[4], b[4];
+        for (int k = 0; k < 64; k++) {
+            const float a = xs[tr][k];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                a[i] = xs[k][tr + i];
-                b[i] = ws[k][tc + i];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
+            for (int j = 0; j < 4; j++) acc[j] += a * ws[tc + j][k];
         }
         __syncthreads();
     }
+    const int tt = t0 + tr;
+    if (tt < T) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int tt = t0 + tr + i, nn = n0 + tc + j;
-            if (tt < T && nn < rows) y[(size_t)tt * ldy + nn] = acc[i][j];
-        }
+        for (int j = 0; j < 4; j++)
+            if (n0 + tc + j < rows) y[(size_t)tt * ldy + n0 + tc + j] = acc[j];
+    }
 }
 
 __global__ void k_cfg_combine(float* __restrict__ v, const float* __restrict__ vn, float cfg, size_t n) {
@@ -187,7 +181,7 @@ hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int 
 }
 hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* W, int T, int rows, int cols,
                              hipStream_t s) {
-    hipLaunchKernelGGL(k_linear_f32, dim3((rows + 63) / 64, (T + 63) / 64), dim3(256), 0, s, y, ldy, x, ldx, W, T,
+    hipLaunchKernelGGL(k_linear_f32, dim3((rows + 63) / 64, (T + 15) / 16), dim3(256), 0, s, y, ldy, x, ldx, W, T,
                        rows, cols);
     return hipGetLastError();
 }

@@ -253,6 +253,16 @@ int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const 
                         const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,
                         float nag_scale, float nag_tau, float nag_alpha, kiln_stream_t stream);
 
+/* The DiT cross-attention section from the block's fp16 LayerNorm output (engine/src/dit.cu:475-487): the cross
+ * Q projection (wq_prepped: kiln_linear16_prepare_weight of ca_q [D, D]) with the Q RMSNorm fused into its
+ * epilogue (fp16 Q, pre-scaled), then kiln_cross_attn_nag's attention and NAG with those Q. workspace: B*T*D*2
+ * bytes (the fp16 Q), 16-byte aligned. Other arguments as kiln_cross_attn_nag. */
+int kiln_dit_cross_attn_x16(void* out, void* out_neg, int out_dtype, int ldo, const uint16_t* x16,
+                            const uint16_t* wq_prepped, const uint16_t* q_norm_w, float eps, int B, int T, int H,
+                            const uint16_t* const* kvp, const int* Lk, const int* npad, const uint16_t* kvp_neg,
+                            int Lk_neg, int npad_neg, float nag_scale, float nag_tau, float nag_alpha, void* workspace,
+                            size_t ws_bytes, kiln_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

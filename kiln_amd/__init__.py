@@ -67,6 +67,8 @@ _SIGS = {
     "kiln_dit_self_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "kiln_dit_self_attn_x16": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "kiln_dit_self_attn_x16_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kiln_dit_cross_attn_x16": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _f,
+                                     _f, _f, _vp, _sz, _vp]),
     "kiln_cross_attn_nag": (_i, [_vp, _vp, _i, _i, _vp, _i, _i, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _f,
                                  _f, _f, _vp]),
 }
@@ -427,4 +429,23 @@ def torch_randn(seed, n):
     import torch
     out = torch.empty(n, dtype=torch.float32)
     _check(lib().kiln_torch_randn(_ptr(out), seed, n))
+    return out
+
+
+def dit_cross_attn_x16(out, x16, wq, B, T, H, kvps, Lks, npads, q_norm_w, eps=1e-6, kvp_neg=None, Lk_neg=0,
+                       npad_neg=0, out_neg=None, scale=5.0, tau=2.5, alpha=0.25, workspace=None, stream=None):
+    """The DiT cross-attention section from the fp16 LayerNorm output: cross-Q projection (wq: a PreppedWeight)
+    with the Q RMSNorm in its epilogue, then cross-attention + NAG (kiln_dit_cross_attn_x16)."""
+    import torch
+    D = H * 128
+    if workspace is None:
+        workspace = torch.empty(B * T * D * 2, dtype=torch.uint8, device=x16.device)
+    n = len(kvps)
+    ptrs = (ctypes.c_void_p * n)(*[k.data_ptr() for k in kvps])
+    lks = (ctypes.c_int * n)(*Lks)
+    nps = (ctypes.c_int * n)(*npads)
+    _check(lib().kiln_dit_cross_attn_x16(_ptr(out), _ptr(out_neg), _dt(out), _ld(out), _ptr(x16), _ptr(wq.buf),
+                                         _bf16_bits(q_norm_w), eps, B, T, H, ctypes.cast(ptrs, _vp),
+                                         ctypes.cast(lks, _vp), ctypes.cast(nps, _vp), _ptr(kvp_neg), Lk_neg, npad_neg,
+                                         scale, tau, alpha, _ptr(workspace), workspace.numel(), _stream(stream)))
     return out

@@ -424,10 +424,10 @@ int kiln_dit_self_attn_x16(void* out, int out_dtype, int ldo, const uint16_t* x1
     return hip_check(kiln::launch_attn_fwd(a, s), "attn_fwd launch");
 }
 
-int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
-                        const uint16_t* q_norm_w, float eps, int B, int T, int H, const uint16_t* const* kvp,
-                        const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,
-                        float nag_scale, float nag_tau, float nag_alpha, kiln_stream_t stream) {
+static int cross_attn_impl(void* out, void* out_neg, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
+                           const uint16_t* q_norm_w, float eps, int B, int T, int H, const uint16_t* const* kvp,
+                           const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,
+                           float nag_scale, float nag_tau, float nag_alpha, bool q_prescaled, kiln_stream_t stream) {
     if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
         return fail(KILN_EINVAL, "dtype");
     const int nj = B + (kvp_neg ? 1 : 0);
@@ -459,11 +459,53 @@ int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const 
     a.out = od;
     a.qw = q_norm_w;
     a.eps = eps;
+    a.q_prescaled = q_prescaled;
     int r = hip_check(kiln::launch_attn_fwd(a, (hipStream_t)stream), "attn_fwd launch");
     if (r || !kvp_neg) return r;
     return hip_check(kiln::launch_nag(out, ldo, out_neg, ldo, od, T, H * 128, nag_scale, nag_tau, nag_alpha,
                                       (hipStream_t)stream),
                      "nag launch");
+}
+
+int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
+                        const uint16_t* q_norm_w, float eps, int B, int T, int H, const uint16_t* const* kvp,
+                        const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,
+                        float nag_scale, float nag_tau, float nag_alpha, kiln_stream_t stream) {
+    return cross_attn_impl(out, out_neg, out_dtype, ldo, q, in_dtype, ldq, q_norm_w, eps, B, T, H, kvp, Lk, npad,
+                           kvp_neg, Lk_neg, npad_neg, nag_scale, nag_tau, nag_alpha, false, stream);
+}
+
+int kiln_dit_cross_attn_x16(void* out, void* out_neg, int out_dtype, int ldo, const uint16_t* x16,
+                            const uint16_t* wq_prepped, const uint16_t* q_norm_w, float eps, int B, int T, int H,
+                            const uint16_t* const* kvp, const int* Lk, const int* npad, const uint16_t* kvp_neg,
+                            int Lk_neg, int npad_neg, float nag_scale, float nag_tau, float nag_alpha, void* workspace,
+                            size_t ws_bytes, kiln_stream_t stream) {
+    if (B <= 0 || T <= 0 || H <= 0 || H % 2) return fail(KILN_EINVAL, "bad sizes B=%d T=%d H=%d (H even)", B, T, H);
+    if (!x16 || !wq_prepped || !q_norm_w || !workspace) return fail(KILN_EINVAL, "null pointer");
+    if (!aligned16(x16) || !aligned16(wq_prepped) || !aligned16(workspace))
+        return fail(KILN_EUNSUPPORTED, "operands not 16-byte aligned");
+    const int D = H * kiln::HD;
+    if (ws_bytes < (size_t)B * T * D * 2) return fail(KILN_ENOMEM, "workspace %zu < %zu bytes", ws_bytes, (size_t)B * T * D * 2);
+    uint16_t* q16 = static_cast<uint16_t*>(workspace);
+    kiln::GemmLaunch g{};
+    g.a = x16;
+    g.w = wq_prepped;
+    g.K = D;
+    g.M = B * T;
+    g.N = D;
+    g.ldc = D;
+    g.epi = 4;
+    g.wprep = true;
+    g.q16 = q16;
+    g.T = T;
+    g.H = H;
+    g.qw = q_norm_w;
+    g.kw = q_norm_w;
+    g.eps = eps;
+    int rc = hip_check(kiln::launch_gemm16(g, (hipStream_t)stream), "cross-Q projection launch");
+    if (rc) return rc;
+    return cross_attn_impl(out, out_neg, out_dtype, ldo, q16, KILN_F16, D, nullptr, eps, B, T, H, kvp, Lk, npad, kvp_neg,
+                           Lk_neg, npad_neg, nag_scale, nag_tau, nag_alpha, true, stream);
 }
 
 int kiln_rmsnorm_rows(float* y, const float* x, const uint16_t* w_bf16, int rows, int dim, float eps,

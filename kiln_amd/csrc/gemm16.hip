@@ -166,10 +166,11 @@ __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)
             for (int nb = 0; nb < NBW; nb++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[nb][mb][e] *= r[mb] * wt[nb][e];
-        // RoPE partner exchange, two row blocks per round: [wave][mb in round][nb][lane][e]
+        // RoPE partner exchange, two row blocks per round: [wave][mb in round][nb][lane][e] (no tables: no RoPE,
+        // the cross-attention Q projection)
         constexpr int XW = 2 * NBW * 64 * 4;  // floats per wave per round
 #pragma unroll
-        for (int g0 = 0; g0 < MB; g0 += 2) {
+        for (int g0 = 0; g0 < (p.rcos ? MB : 0); g0 += 2) {
             __syncthreads();
 #pragma unroll
             for (int j = 0; j < 2; j++)

@@ -8,8 +8,8 @@ Mirrors the block loop of the reference's Dit::forward_batch for G.fp16 && G.tc1
                                                   then one attention launch (kiln_dit_self_attn_x16)
     X += gate * linear16(A16, sa_o)                                      RESID epilogue
     N16 = layernorm_mod16(X; cross-attention modulation)
-    Q = linear16(N16, ca_q)                                              fp32
-    A16 = attention16(rmsnorm(Q), context K/V of each item) (+ NAG on item 0)   kiln_cross_attn_nag
+    Q = linear16(N16, ca_q)                       epilogue applies the Q RMSNorm, fp16 Q; then the
+    A16 = attention16(rmsnorm(Q), ctx K/V) + NAG  attention of all contexts + NAG (kiln_dit_cross_attn_x16)
     X += gate * linear16(A16, ca_o)
     N16 = layernorm_mod16(X; MLP modulation)
     H16 = GELU(linear16(N16, mlp1))                                      GELU16 epilogue
@@ -23,7 +23,7 @@ Every call below goes to the HIP library; there is no CPU path.
 import numpy as np
 import torch
 
-from . import (KILN_EPI_F32, KILN_EPI_GELU16, KILN_EPI_RESID, add_gated, cross_attn_nag, dit_self_attn_x16,
+from . import (KILN_EPI_GELU16, KILN_EPI_RESID, add_gated, dit_cross_attn_x16, dit_self_attn_x16,
                kv_prepare, layernorm_mod, lib, linear16, linear16_prepare_weight, linear_f32, matvec, matvec_grouped,
                patchify, rel_l1, rmsnorm, silu, sub, unpatchify)
 
@@ -63,7 +63,7 @@ class Workspace:
     def __init__(self, B, T, D, F, device):
         R = B * T
         self.n16 = torch.empty(R, D, dtype=torch.float16, device=device)
-        self.q = torch.empty(R, D, dtype=torch.float32, device=device)
+        self.q16 = torch.empty(R * D * 2, dtype=torch.uint8, device=device)  # fp16 cross-attention Q
         self.a16 = torch.empty(R, D, dtype=torch.float16, device=device)
         self.an16 = torch.empty(T, D, dtype=torch.float16, device=device)
         self.h16 = torch.empty(R, F, dtype=torch.float16, device=device)
@@ -77,21 +77,20 @@ def block_forward16(X, mods, blk, ws, B, T, rope, ctx, nag=None, eps=1e-6):
     tau, alpha) for item 0."""
     D, H = blk.D, blk.D // HD
     mo, mc, mm = mods[0:3 * D], mods[3 * D:6 * D], mods[6 * D:9 * D]
-    q = ws.q
     # self-attention: the Q/K/V projection's epilogue applies the QK-RMSNorm and RoPE and writes fp16 Q and the
     # prepared K/V, then the attention of the B items (kiln_dit_self_attn_x16)
     layernorm_mod(ws.n16, X, mo[D:2 * D], mo[0:D], eps)
     dit_self_attn_x16(ws.a16, ws.n16, blk.sa_qkv, B, T, H, blk.sa_qn, blk.sa_kn, rope, eps=eps, workspace=ws.attn_ws)
     linear16(X, ws.a16, blk.sa_o, epi=KILN_EPI_RESID, gate=mo[2 * D:3 * D])
-    # cross-attention, each item against its own context (+ NAG on item 0)
+    # cross-attention, each item against its own context (+ NAG on item 0): the cross-Q projection's epilogue
+    # applies the Q RMSNorm and writes fp16 Q (kiln_dit_cross_attn_x16)
     layernorm_mod(ws.n16, X, mc[D:2 * D], mc[0:D], eps)
-    linear16(q, ws.n16, blk.ca_q, epi=KILN_EPI_F32)
-    kvps = [c[0] for c in ctx[:B]]
-    args = dict(q_norm_w=blk.ca_qn, eps=eps)
+    args = dict(q_norm_w=blk.ca_qn, eps=eps, workspace=ws.q16)
     if nag is not None:
         args.update(kvp_neg=nag[0], Lk_neg=nag[1], npad_neg=nag[2], out_neg=ws.an16, scale=nag[3], tau=nag[4],
                     alpha=nag[5])
-    cross_attn_nag(ws.a16, q, B, T, H, kvps, [c[1] for c in ctx[:B]], [c[2] for c in ctx[:B]], **args)
+    dit_cross_attn_x16(ws.a16, ws.n16, blk.ca_q, B, T, H, [c[0] for c in ctx[:B]], [c[1] for c in ctx[:B]],
+                       [c[2] for c in ctx[:B]], **args)
     linear16(X, ws.a16, blk.ca_o, epi=KILN_EPI_RESID, gate=mc[2 * D:3 * D])
     # MLP
     layernorm_mod(ws.n16, X, mm[D:2 * D], mm[0:D], eps)

@@ -320,3 +320,28 @@ def test_dit_self_attn_x16_fused_projection(gpu, Hh, Hp_, Wp_, Bb):
         errs.append((out[b * Tt:(b + 1) * Tt][sel.to(DEV)].cpu().double() - ref).abs())
     e = torch.cat(errs)
     assert e.max().item() <= 2e-3 and e.mean().item() <= 2e-4, (e.max().item(), e.mean().item())
+
+
+def test_dit_cross_attn_x16_fused_projection(gpu):
+    """kiln_dit_cross_attn_x16 (cross-Q GEMM with the Q RMSNorm in its epilogue, then cross-attention + NAG)
+    against the unfused path (linear16 F32 + kiln_cross_attn_nag) on the same inputs."""
+    g = torch.Generator().manual_seed(35)
+    x = torch.randn(B * T, D, generator=g).half().to(DEV)
+    wq = (torch.randn(D, D, generator=g) * D ** -0.5).half().to(DEV)
+    qn, kn = (_bf16(1 + 0.2 * torch.randn(HD, generator=g)).to(DEV) for _ in range(2))
+    ctxs = [torch.randn(r, D, generator=g).to(DEV) for r in REALS]
+    kvs = [kiln_amd.kv_prepare(c, c * 0.5, H, k_norm_w=kn) for c in ctxs]
+    wp = kiln_amd.linear16_prepare_weight(wq)
+    out, neg = (torch.empty(n, D, dtype=torch.float16, device=DEV) for n in (B * T, T))
+    args = dict(kvp_neg=kvs[2], Lk_neg=REALS[2], npad_neg=L - REALS[2], scale=5.0, tau=2.5, alpha=0.25)
+    kiln_amd.dit_cross_attn_x16(out, x, wp, B, T, H, kvs[:B], REALS[:B], [L - r for r in REALS[:B]], qn,
+                                out_neg=neg, **args)
+    q = torch.empty(B * T, D, device=DEV)
+    kiln_amd.linear16(q, x, wp)
+    ref, neg2 = torch.empty_like(out), torch.empty_like(neg)
+    kiln_amd.cross_attn_nag(ref, q, B, T, H, kvs[:B], REALS[:B], [L - r for r in REALS[:B]], q_norm_w=qn,
+                            out_neg=neg2, **args)
+    torch.cuda.synchronize()
+    d = (out.float() - ref.float()).abs()
+    assert torch.isfinite(out.float()).all()
+    assert d.max().item() <= 2e-3 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())

@@ -121,6 +121,16 @@ inline void linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_
           "linear16");
 }
 
+// The DiT self-attention section from the block's fp16 LayerNorm output (engine/src/dit.cu:460-469): the
+// stacked Q/K/V projection with QK-RMSNorm, RoPE and K/V preparation in its epilogue, then the attention.
+inline void dit_self_attention_x16(uint16_t* out, int ldo, const uint16_t* x16, const Linear16Weight& wqkv,
+                                   const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps, const float* rcos,
+                                   const float* rsin, int B, int T, int H, void* workspace, size_t ws_bytes) {
+    check(kiln_dit_self_attn_x16(out, KILN_F16, ldo, x16, wqkv.data(), q_norm_w, k_norm_w, eps, rcos, rsin, B, T, H,
+                                 workspace, ws_bytes, (kiln_stream_t)stream_ref()),
+          "dit_self_attn_x16");
+}
+
 // NAG combine of fp16 rows (the k_nag<__half> launch of the fp16-activation forward).
 inline void nag16(uint16_t* a, const uint16_t* an, int T, int dim, float scale, float tau, float alpha) {
     check(kiln_nag_combine(a, dim, an, dim, KILN_F16, T, dim, scale, tau, alpha, (kiln_stream_t)stream_ref()),

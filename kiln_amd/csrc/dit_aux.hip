@@ -7,7 +7,7 @@
 //   silu         y = v / (1 + exp(-v))                                               kernels.cu:735-739
 //   patchify     tok [T, 68] from a 16-channel latent [16, Hl, Wl], 2x2 patches      dit.cu:174-182
 //   unpatchify   latent [16, Hl, Wl] from tok [T, 64]                                dit.cu:184-191
-//   linear_f32   y [T, rows] = x [T, cols] W^T, W bf16 [rows, cols], fp32 math      kernels.cu:508-529 (linear)
+//   linear_f32   y [T, rows] = x [T, cols] W^T, W bf16 [rows, cols], fp32 MFMA      kernels.cu:508-529 (linear)
 //   cfg_combine  v = vn + cfg (v - vn)                                              kernels.cu:1058-1062
 #include "common.hpp"
 #include "internal.hpp"
@@ -74,38 +74,95 @@ __global__ void k_unpatchify(float* __restrict__ lat, const float* __restrict__ 
     lat[((size_t)c * Hl + yy) * Wl + xx] = tok[(size_t)t * ldt + f];
 }
 
-// y [T, rows] (row stride ldy) = x [T, cols] (row stride ldx) W^T: 16 x 64 output tiles (enough workgroups for the
-// final layer's 64 output columns), k in chunks of 64 through LDS, each thread 4 outputs of one row in fp32.
+// y [T, rows] (row stride ldy) = x [T, cols] (row stride ldx) W^T on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32: fp32 products, fp32 accumulation). One wave per 16 rows x 64 output columns; k in
+// chunks of 32: lane (i = lane % 16, g = lane / 16) holds x[i][k0 + 8g .. 8g + 8) and, for each of the 4 column
+// blocks, W[j = i][k0 + 8g .. 8g + 8), and MFMA step s of the chunk takes element s of both (the same k on the
+// A and the B side). Out-of-range rows and k read as 0.
 __global__ __launch_bounds__(256) void k_linear_f32(float* __restrict__ y, int ldy, const float* __restrict__ x,
                                                     int ldx, const uint16_t* __restrict__ W, int T, int rows, int cols) {
-    __shared__ float xs[16][65];
-    __shared__ float ws[64][65];
-    const int t0 = blockIdx.y * 16, n0 = blockIdx.x * 64, tid = threadIdx.x;
-    const int tr = tid >> 4, tc = (tid & 15) * 4;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < cols; k0 += 64) {
-        for (int e = tid; e < 16 * 64; e += 256) {
-            const int r = e >> 6, k = e & 63, tt = t0 + r, kk = k0 + k;
-            xs[r][k] = (tt < T && kk < cols) ? x[(size_t)tt * ldx + kk] : 0.f;
-        }
-        for (int e = tid; e < 64 * 64; e += 256) {
-            const int r = e >> 6, k = e & 63, nn = n0 + r, kk = k0 + k;
-            ws[r][k] = (nn < rows && kk < cols) ? bf16_to_f32(W[(size_t)nn * cols + kk]) : 0.f;
-        }
-        __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < 64; k++) {
-            const float a = xs[tr][k];
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nt = (rows + 63) / 64;
+    const int t0 = (wave / nt) * 16, n0 = (wave % nt) * 64;
+    if (t0 >= T) return;
+    const int i = lane & 15, g = lane >> 4;
+    const int tr = t0 + i;
+    const float* xr = x + (size_t)min(tr, T - 1) * ldx;
+    floatx4 acc[4] = {};
+    const uint16_t* wr[4];
+    bool nin[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[j] += a * ws[tc + j][k];
-        }
-        __syncthreads();
+    for (int nb = 0; nb < 4; nb++) {
+        const int n = n0 + nb * 16 + i;
+        nin[nb] = n < rows;
+        wr[nb] = W + (size_t)min(n, rows - 1) * cols;
     }
-    const int tt = t0 + tr;
-    if (tt < T) {
+    // vector loads (16 bytes of x, 16 bytes of W per lane and block) for whole chunks when rows are 16-byte
+    // aligned; element loads with bounds for the tail chunk and unaligned rows
+    const bool vec = ((cols & 7) == 0) && ((ldx & 3) == 0) && (((size_t)x & 15) == 0) && (((size_t)W & 15) == 0);
+    const int kfull = vec ? cols / 32 * 32 : 0;
+    float xa[2][8], wv[2][4][8];
+    auto load = [&](int k0, float(&xo)[8], float(&wo)[4][8]) {
+        const int kb = k0 + 8 * g;
+        const floatx4 a0 = *reinterpret_cast<const floatx4*>(xr + kb);
+        const floatx4 a1 = *reinterpret_cast<const floatx4*>(xr + kb + 4);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (n0 + tc + j < rows) y[(size_t)tt * ldy + n0 + tc + j] = acc[j];
+        for (int e = 0; e < 4; e++) {
+            xo[e] = tr < T ? a0[e] : 0.f;
+            xo[e + 4] = tr < T ? a1[e] : 0.f;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(wr[nb] + kb);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                wo[nb][2 * e] = nin[nb] ? __uint_as_float(raw[e] << 16) : 0.f;
+                wo[nb][2 * e + 1] = nin[nb] ? __uint_as_float(raw[e] & 0xffff0000u) : 0.f;
+            }
+        }
+    };
+    auto mma = [&](const float(&xo)[8], const float(&wo)[4][8]) {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xo[e], wo[nb][e], acc[nb], 0, 0, 0);
+    };
+    int k0 = 0;
+    if (kfull > 0) {
+        load(0, xa[0], wv[0]);
+        for (; k0 + 32 < kfull; k0 += 64) {  // the next chunk's loads in flight during this chunk's MFMAs
+            load(k0 + 32, xa[1], wv[1]);
+            mma(xa[0], wv[0]);
+            if (k0 + 64 < kfull) load(k0 + 64, xa[0], wv[0]);
+            mma(xa[1], wv[1]);
+        }
+        if (k0 < kfull) {
+            mma(xa[0], wv[0]);
+            k0 += 32;
+        }
+    }
+    for (; k0 < cols; k0 += 32) {
+        const int kb = k0 + 8 * g;
+        float xo[8], wo[4][8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) xo[e] = (tr < T && kb + e < cols) ? xr[kb + e] : 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) wo[nb][e] = (nin[nb] && kb + e < cols) ? bf16_to_f32(wr[nb][kb + e]) : 0.f;
+        mma(xo, wo);
+    }
+    // lane holds column n0 + nb*16 + i of rows t0 + 4g + r
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+        const int n = n0 + nb * 16 + i;
+        if (n >= rows) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int t = t0 + 4 * g + r;
+            if (t < T) y[(size_t)t * ldy + n] = acc[nb][r];
+        }
     }
 }
 
@@ -181,8 +238,9 @@ hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int 
 }
 hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* W, int T, int rows, int cols,
                              hipStream_t s) {
-    hipLaunchKernelGGL(k_linear_f32, dim3((rows + 63) / 64, (T + 15) / 16), dim3(256), 0, s, y, ldy, x, ldx, W, T,
-                       rows, cols);
+    const long waves = (long)((T + 15) / 16) * ((rows + 63) / 64);
+    hipLaunchKernelGGL(k_linear_f32, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, y, ldy, x, ldx, W, T, rows,
+                       cols);
     return hipGetLastError();
 }
 hipError_t launch_cfg_combine(float* v, const float* vn, float cfg, size_t n, hipStream_t s) {

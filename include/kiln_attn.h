@@ -172,6 +172,11 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
 /* One Euler step of the velocity v without a mask (engine/src/pipeline.cu:318-331, k_denoised then
  * k_euler_step): den = x - v * sigma; x = x + (x - den) / sigma * (sigma_next - sigma). sigma > 0. */
 int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next, size_t n, kiln_stream_t stream);
+/* The sampler's denoised estimate without a mask (engine/src/pipeline.cu:318-324): den = x - v * sigma. */
+int kiln_flow_denoised(float* den, const float* x, const float* v, float sigma, size_t n, kiln_stream_t stream);
+/* The generic sampler step (engine/src/pipeline.cu:333-337, k_update): x = a x + b den + c old (old NULL: 0). */
+int kiln_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
+                     kiln_stream_t stream);
 /* Replaces cfg_combine() (engine/src/gpu.h:144, kernels.cu:1058-1062): v = vn + cfg * (v - vn), n elements. */
 int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream_t stream);
 

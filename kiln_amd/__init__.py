@@ -48,6 +48,8 @@ _SIGS = {
     "kiln_rel_l1": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "kiln_torch_randn": (_i, [_vp, ctypes.c_uint64, _sz]),
     "kiln_flow_start": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
+    "kiln_flow_denoised": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
+    "kiln_flow_update": (_i, [_vp, _vp, _vp, _f, _f, _f, _sz, _vp]),
     "kiln_flow_euler_step": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "kiln_linear16_prepped_weight_bytes": (_sz, [_i, _i]),
@@ -449,3 +451,15 @@ def dit_cross_attn_x16(out, x16, wq, B, T, H, kvps, Lks, npads, q_norm_w, eps=1e
                                          ctypes.cast(lks, _vp), ctypes.cast(nps, _vp), _ptr(kvp_neg), Lk_neg, npad_neg,
                                          scale, tau, alpha, _ptr(workspace), workspace.numel(), _stream(stream)))
     return out
+
+
+def flow_denoised(den, x, v, sigma, stream=None):
+    """k_denoised without a mask (engine/src/pipeline.cu:318-324): den = x - v sigma."""
+    _check(lib().kiln_flow_denoised(_ptr(den), _ptr(x), _ptr(v), sigma, x.numel(), _stream(stream)))
+    return den
+
+
+def flow_update(x, den, a, b, old=None, c=0.0, stream=None):
+    """k_update (engine/src/pipeline.cu:333-337): x = a x + b den + c old."""
+    _check(lib().kiln_flow_update(_ptr(x), _ptr(den), _ptr(old), a, b, c, x.numel(), _stream(stream)))
+    return x

@@ -678,6 +678,19 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
     return hip_check(kiln::launch_flow_start(x, noise, init, sigma, n, (hipStream_t)stream), "flow_start launch");
 }
 
+int kiln_flow_denoised(float* den, const float* x, const float* v, float sigma, size_t n, kiln_stream_t stream) {
+    if (n && (!den || !x || !v)) return fail(KILN_EINVAL, "flow_denoised: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_flow_denoised(den, x, v, sigma, n, (hipStream_t)stream), "flow_denoised launch");
+}
+
+int kiln_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
+                     kiln_stream_t stream) {
+    if (n && (!x || !den)) return fail(KILN_EINVAL, "flow_update: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_flow_update(x, den, old, a, b, c, n, (hipStream_t)stream), "flow_update launch");
+}
+
 int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next, size_t n, kiln_stream_t stream) {
     if (n && (!x || !v)) return fail(KILN_EINVAL, "flow_euler_step: null pointer");
     if (!(sigma > 0.f)) return fail(KILN_EINVAL, "flow_euler_step: sigma %g must be > 0", (double)sigma);

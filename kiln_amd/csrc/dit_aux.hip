@@ -213,6 +213,19 @@ __global__ __launch_bounds__(256) void k_rel_l1(const float* __restrict__ a, con
     }
 }
 
+// the sampler's denoised estimate without a mask (pipeline.cu:318-324) and the generic sampler step
+// x <- a x + b den + c old (pipeline.cu:333-337, k_update; old may be null)
+__global__ void k_flow_denoised(float* __restrict__ den, const float* __restrict__ x, const float* __restrict__ v,
+                                float s, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) den[i] = x[i] - v[i] * s;
+}
+__global__ void k_flow_update(float* __restrict__ x, const float* __restrict__ den, const float* __restrict__ old,
+                              float a, float b, float c, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = a * x[i] + b * den[i] + (old ? c * old[i] : 0.f);
+}
+
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
@@ -264,6 +277,16 @@ hipError_t launch_sub(float* y, const float* a, const float* b, size_t n, hipStr
 hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, hipStream_t st) {
     hipLaunchKernelGGL(k_zero2, dim3(1), dim3(64), 0, st, acc);
     hipLaunchKernelGGL(k_rel_l1, dim3(512), dim3(256), 0, st, a, b, n, acc);
+    return hipGetLastError();
+}
+
+hipError_t launch_flow_denoised(float* den, const float* x, const float* v, float s, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_denoised, dim3(nblk(n)), dim3(256), 0, st, den, x, v, s, n);
+    return hipGetLastError();
+}
+hipError_t launch_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
+                              hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_update, dim3(nblk(n)), dim3(256), 0, st, x, den, old, a, b, c, n);
     return hipGetLastError();
 }
 

@@ -101,6 +101,9 @@ hipError_t launch_cfg_combine(float* v, const float* vn, float cfg, size_t n, hi
 hipError_t launch_sub(float* y, const float* a, const float* b, size_t n, hipStream_t st);
 hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, hipStream_t st);
 hipError_t launch_flow_start(float* x, const float* noise, const float* init, float s, size_t n, hipStream_t st);
+hipError_t launch_flow_denoised(float* den, const float* x, const float* v, float s, size_t n, hipStream_t st);
+hipError_t launch_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
+                              hipStream_t st);
 hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st);
 
 // torch.manual_seed(seed); torch.randn(n) on the host (host_rng.cpp); false if n < 16

@@ -10,7 +10,7 @@ import math
 
 import numpy as np
 
-from . import cfg_combine, flow_euler_step, flow_start
+from . import cfg_combine, flow_denoised, flow_euler_step, flow_start, flow_update, torch_randn
 
 
 def flow_sigmas(steps, shift=1.0, denoise=1.0):
@@ -26,6 +26,27 @@ def flow_sigmas(steps, shift=1.0, denoise=1.0):
     return s[len(s) - (steps + 1):]
 
 
+SAMPLERS = ("euler", "euler_ancestral", "dpmpp_2m", "res_multistep")
+
+
+def step_coef(sampler, sig, i, have_old):
+    """(a, b, c) of the step x <- a x + b den + c old from sigma_i to sigma_{i+1} (engine/src/pipeline.cu:396-411):
+    first order (Euler) without history or at sigma 0; dpmpp_2m and res_multistep (eta 0) in log-sigma time."""
+    s, sn = float(sig[i]), float(sig[i + 1])
+    if sampler == "euler" or not have_old or sn == 0.0:
+        return sn / s, 1.0 - sn / s, 0.0
+    t, tn, tp = -math.log(s), -math.log(sn), -math.log(float(sig[i - 1]))
+    h = tn - t
+    if sampler == "dpmpp_2m":
+        r = (t - tp) / h
+        b = -math.expm1(-h)
+        return sn / s, b * (1.0 + 1.0 / (2.0 * r)), -b / (2.0 * r)
+    c2 = (tp - t) / h
+    phi1 = math.expm1(-h) / (-h)
+    phi2 = (phi1 - 1.0) / (-h)
+    return math.exp(-h), h * (phi1 - phi2 / c2), h * (phi2 / c2)
+
+
 def initial_noise(seed, shape, device):
     """The sampler's noise (engine/src/pipeline.cu:428-429): torch_randn(seed, n) on the host, then to the device."""
     from . import torch_randn
@@ -36,10 +57,12 @@ def initial_noise(seed, shape, device):
 
 
 def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=1.0, init=None, negative=True,
-                 cache=None, cache_start=0.15, cache_end=0.9, cache_max_hits=2):
+                 cache=None, cache_start=0.15, cache_end=0.9, cache_max_hits=2, sampler="euler", seed=0):
     """model(outs, x, t, cfg_now) writes the velocity of the prompt into outs[0] and, when cfg_now, of the
     negative context into outs[1]; x [16, Hl, Wl] fp32 (overwritten with the result), noise like x;
     negative: whether a negative context exists (CFG runs for the first ceil(cfg_until * steps) steps).
+    sampler: "euler" (k_euler_step's arithmetic), "euler_ancestral" (the RF ancestral step with eta 1, fresh
+    noise torch_randn(seed + 1 + i) per step, pipeline.cu:514-529), "dpmpp_2m" or "res_multistep" (step_coef).
     cache: a kiln_amd.dit.StepCache the model's forward uses, or None; the sampler allows a skip only after the
     first max(2, ceil(cache_start * steps)) steps, before the last max(1, ceil((1 - cache_end) * steps)), and
     for at most cache_max_hits steps in a row (engine/src/pipeline.cu:463-480, 488, 506-509). Returns x; the
@@ -50,7 +73,11 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
         if init is not None:
             x.copy_(init)
         return x
+    if sampler not in SAMPLERS:
+        raise ValueError(f"unknown sampler {sampler}")
     v, vn = torch.empty_like(x), torch.empty_like(x)
+    den, old = torch.empty_like(x), torch.empty_like(x)
+    have_old = False
     cfg_steps = math.ceil(cfg_until * steps - 1e-4) if negative else 0
     warm = max(2, math.ceil(cache_start * steps))
     tail = max(1, math.ceil((1.0 - cache_end) * steps))
@@ -73,5 +100,26 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
                 run = 0
         if cfg_now:
             cfg_combine(v, vn, cfg)
-        flow_euler_step(x, v, s, sigmas[i + 1])
+        sn = sigmas[i + 1]
+        if sampler == "euler":
+            flow_euler_step(x, v, s, sn)
+        elif sampler == "euler_ancestral":
+            flow_denoised(den, x, v, s)
+            if sn == 0.0:
+                flow_update(x, den, 0.0, 1.0)
+            else:
+                sd = sn * (1.0 + (sn / s - 1.0))
+                aip1, ad = 1.0 - sn, 1.0 - sd
+                renoise = math.sqrt(max(0.0, sn * sn - sd * sd * aip1 * aip1 / (ad * ad)))
+                r, a = sd / s, aip1 / ad
+                flow_update(x, den, a * r, a * (1.0 - r))
+                nz = torch_randn(seed + 1 + i, x.numel()).view_as(x).to(x.device)
+                flow_update(x, nz, 1.0, renoise)
+        else:
+            flow_denoised(den, x, v, s)
+            a, b, c = step_coef(sampler, sigmas, i, have_old)
+            flow_update(x, den, a, b, old if have_old else None, c)
+        if sampler != "euler":
+            den, old = old, den
+            have_old = True
     return x

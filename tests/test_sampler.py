@@ -86,3 +86,50 @@ def test_step_cache_guards(gpu):
     expect = [False] * 3 + [True, True, False] * 5
     expect = (expect + [False] * 20)[:18] + [False, False]
     assert stub.allowed == expect and sc.skips == sum(expect)
+
+
+@pytest.mark.parametrize("name", ["euler", "dpmpp_2m", "res_multistep"])
+def test_step_coef_exact_on_linear_trajectories(name):
+    """Every step x <- a x + b den + c old (engine/src/pipeline.cu:396-411) must keep a point of a straight flow
+    trajectory x(s) = x0 + s (n - x0) on it when den = old = x0: a = s'/s and b + c = 1 - s'/s."""
+    sig = sampler.flow_sigmas(10, 3.0)
+    for i in range(10):
+        a, b, c = sampler.step_coef(name, sig, i, i > 0)
+        sn, s = sig[i + 1], sig[i]
+        assert abs(a - sn / s) < 1e-12 and abs(b + c - (1 - sn / s)) < 1e-12
+    # first step and the step to sigma 0 are first order
+    assert sampler.step_coef(name, sig, 0, False)[2] == 0.0 and sampler.step_coef(name, sig, 9, True)[2] == 0.0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["euler", "dpmpp_2m", "res_multistep", "euler_ancestral"])
+def test_samplers_on_a_straight_trajectory(gpu, name):
+    """A model with constant velocity v = n - x0 (a straight trajectory from the noise n to x0): the
+    deterministic samplers land on x0; the ancestral one against a float64 statement of its step with the
+    library's torch_randn noise."""
+    g = torch.Generator().manual_seed(11)
+    x0, n = torch.randn(16, 4, 6, generator=g), torch.randn(16, 4, 6, generator=g)
+    vd = (n - x0).to(DEV)
+
+    def model(outs, xx, t, cfg_now):
+        outs[0].copy_(vd)
+
+    sig = sampler.flow_sigmas(6, 3.0)
+    x = torch.empty(16, 4, 6, device=DEV)
+    sampler.sample_euler(model, x, n.to(DEV), sig, negative=False, sampler=name, seed=5)
+    if name != "euler_ancestral":
+        np.testing.assert_allclose(x.cpu().numpy(), x0.numpy(), rtol=0, atol=2e-5)
+        return
+    xr, v = sig[0] * n.double(), (n - x0).double()
+    for i in range(6):
+        s, sn = sig[i], sig[i + 1]
+        den = xr - v * s
+        if sn == 0.0:
+            xr = den
+            continue
+        sd = sn * (1.0 + (sn / s - 1.0))
+        aip1, ad = 1.0 - sn, 1.0 - sd
+        renoise = max(0.0, sn * sn - sd * sd * aip1 * aip1 / (ad * ad)) ** 0.5
+        r, a = sd / s, aip1 / ad
+        xr = a * r * xr + a * (1 - r) * den + renoise * kiln_amd.torch_randn(5 + 1 + i, xr.numel()).view_as(xr).double()
+    np.testing.assert_allclose(x.cpu().double().numpy(), xr.numpy(), rtol=0, atol=2e-5)

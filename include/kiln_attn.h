@@ -174,6 +174,13 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
 int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next, size_t n, kiln_stream_t stream);
 /* The sampler's denoised estimate without a mask (engine/src/pipeline.cu:318-324): den = x - v * sigma. */
 int kiln_flow_denoised(float* den, const float* x, const float* v, float sigma, size_t n, kiln_stream_t stream);
+/* Inpainting (engine/src/pipeline.cu:309-324), latents [16, P] and mask [P]: the model input
+ * xin = m x + (1 - m) (sigma noise + (1 - sigma) init) (k_inpaint_in), and the denoised estimate pinned to the
+ * init outside the mask, den = m (xin - v sigma) + (1 - m) init (k_denoised with a mask). */
+int kiln_flow_inpaint_in(float* xin, const float* x, const float* noise, const float* init, const float* mask,
+                         float sigma, int P, kiln_stream_t stream);
+int kiln_flow_denoised_masked(float* den, const float* xin, const float* v, const float* init, const float* mask,
+                              float sigma, int P, kiln_stream_t stream);
 /* The generic sampler step (engine/src/pipeline.cu:333-337, k_update): x = a x + b den + c old (old NULL: 0). */
 int kiln_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
                      kiln_stream_t stream);

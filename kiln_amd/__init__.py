@@ -48,6 +48,8 @@ _SIGS = {
     "kiln_rel_l1": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "kiln_torch_randn": (_i, [_vp, ctypes.c_uint64, _sz]),
     "kiln_flow_start": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
+    "kiln_flow_inpaint_in": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _vp]),
+    "kiln_flow_denoised_masked": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _vp]),
     "kiln_flow_denoised": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
     "kiln_flow_update": (_i, [_vp, _vp, _vp, _f, _f, _f, _sz, _vp]),
     "kiln_flow_euler_step": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
@@ -463,3 +465,17 @@ def flow_update(x, den, a, b, old=None, c=0.0, stream=None):
     """k_update (engine/src/pipeline.cu:333-337): x = a x + b den + c old."""
     _check(lib().kiln_flow_update(_ptr(x), _ptr(den), _ptr(old), a, b, c, x.numel(), _stream(stream)))
     return x
+
+
+def flow_inpaint_in(xin, x, noise, init, mask, sigma, stream=None):
+    """k_inpaint_in (engine/src/pipeline.cu:309-315): latents [16, ...], mask [P] per pixel."""
+    _check(lib().kiln_flow_inpaint_in(_ptr(xin), _ptr(x), _ptr(noise), _ptr(init), _ptr(mask), sigma, mask.numel(),
+                                      _stream(stream)))
+    return xin
+
+
+def flow_denoised_masked(den, xin, v, init, mask, sigma, stream=None):
+    """k_denoised with a mask (engine/src/pipeline.cu:317-324): pinned to init where the mask is 0."""
+    _check(lib().kiln_flow_denoised_masked(_ptr(den), _ptr(xin), _ptr(v), _ptr(init), _ptr(mask), sigma, mask.numel(),
+                                           _stream(stream)))
+    return den

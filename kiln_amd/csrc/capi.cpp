@@ -678,6 +678,22 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
     return hip_check(kiln::launch_flow_start(x, noise, init, sigma, n, (hipStream_t)stream), "flow_start launch");
 }
 
+int kiln_flow_inpaint_in(float* xin, const float* x, const float* noise, const float* init, const float* mask,
+                         float sigma, int P, kiln_stream_t stream) {
+    if (P < 0 || (P && (!xin || !x || !noise || !init || !mask))) return fail(KILN_EINVAL, "flow_inpaint_in: bad args");
+    if (!P) return KILN_OK;
+    return hip_check(kiln::launch_flow_inpaint_in(xin, x, noise, init, mask, sigma, P, (hipStream_t)stream),
+                     "flow_inpaint_in launch");
+}
+
+int kiln_flow_denoised_masked(float* den, const float* xin, const float* v, const float* init, const float* mask,
+                              float sigma, int P, kiln_stream_t stream) {
+    if (P < 0 || (P && (!den || !xin || !v || !init || !mask))) return fail(KILN_EINVAL, "flow_denoised_masked: bad args");
+    if (!P) return KILN_OK;
+    return hip_check(kiln::launch_flow_denoised_masked(den, xin, v, init, mask, sigma, P, (hipStream_t)stream),
+                     "flow_denoised_masked launch");
+}
+
 int kiln_flow_denoised(float* den, const float* x, const float* v, float sigma, size_t n, kiln_stream_t stream) {
     if (n && (!den || !x || !v)) return fail(KILN_EINVAL, "flow_denoised: null pointer");
     if (!n) return KILN_OK;

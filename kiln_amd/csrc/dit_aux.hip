@@ -226,6 +226,25 @@ __global__ void k_flow_update(float* __restrict__ x, const float* __restrict__ d
     if (i < n) x[i] = a * x[i] + b * den[i] + (old ? c * old[i] : 0.f);
 }
 
+// inpainting (pipeline.cu:309-324): the model input regenerates where m = 1 and is the init re-noised to this
+// sigma where m = 0; the denoised estimate is pinned to the init outside the mask. mask [P] per pixel of the
+// 16-channel latent [16, P].
+__global__ void k_flow_inpaint_in(float* __restrict__ xin, const float* __restrict__ x, const float* __restrict__ noise,
+                                  const float* __restrict__ init, const float* __restrict__ mask, float s, int P) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)16 * P) return;
+    const float m = mask[i % P];
+    xin[i] = m * x[i] + (1.f - m) * (s * noise[i] + (1.f - s) * init[i]);
+}
+__global__ void k_flow_denoised_masked(float* __restrict__ den, const float* __restrict__ xin,
+                                       const float* __restrict__ v, const float* __restrict__ init,
+                                       const float* __restrict__ mask, float s, int P) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)16 * P) return;
+    const float d = xin[i] - v[i] * s, m = mask[i % P];
+    den[i] = m * d + (1.f - m) * init[i];
+}
+
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
@@ -280,6 +299,17 @@ hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, h
     return hipGetLastError();
 }
 
+hipError_t launch_flow_inpaint_in(float* xin, const float* x, const float* noise, const float* init, const float* mask,
+                                  float s, int P, hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_inpaint_in, dim3(nblk((size_t)16 * P)), dim3(256), 0, st, xin, x, noise, init, mask, s, P);
+    return hipGetLastError();
+}
+hipError_t launch_flow_denoised_masked(float* den, const float* xin, const float* v, const float* init,
+                                      const float* mask, float s, int P, hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_denoised_masked, dim3(nblk((size_t)16 * P)), dim3(256), 0, st, den, xin, v, init, mask,
+                       s, P);
+    return hipGetLastError();
+}
 hipError_t launch_flow_denoised(float* den, const float* x, const float* v, float s, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(k_flow_denoised, dim3(nblk(n)), dim3(256), 0, st, den, x, v, s, n);
     return hipGetLastError();

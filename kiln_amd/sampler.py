@@ -10,7 +10,8 @@ import math
 
 import numpy as np
 
-from . import cfg_combine, flow_denoised, flow_euler_step, flow_start, flow_update, torch_randn
+from . import (cfg_combine, flow_denoised, flow_denoised_masked, flow_euler_step, flow_inpaint_in, flow_start,
+               flow_update, torch_randn)
 
 
 def flow_sigmas(steps, shift=1.0, denoise=1.0):
@@ -57,12 +58,14 @@ def initial_noise(seed, shape, device):
 
 
 def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=1.0, init=None, negative=True,
-                 cache=None, cache_start=0.15, cache_end=0.9, cache_max_hits=2, sampler="euler", seed=0):
+                 cache=None, cache_start=0.15, cache_end=0.9, cache_max_hits=2, sampler="euler", seed=0, mask=None):
     """model(outs, x, t, cfg_now) writes the velocity of the prompt into outs[0] and, when cfg_now, of the
     negative context into outs[1]; x [16, Hl, Wl] fp32 (overwritten with the result), noise like x;
     negative: whether a negative context exists (CFG runs for the first ceil(cfg_until * steps) steps).
     sampler: "euler" (k_euler_step's arithmetic), "euler_ancestral" (the RF ancestral step with eta 1, fresh
     noise torch_randn(seed + 1 + i) per step, pipeline.cu:514-529), "dpmpp_2m" or "res_multistep" (step_coef).
+    mask: inpainting mask [Hl, Wl] (1 = regenerate) with init: the model sees the init re-noised to each sigma
+    outside the mask and the denoised estimate is pinned to the init there (pipeline.cu:309-324, 485, 512).
     cache: a kiln_amd.dit.StepCache the model's forward uses, or None; the sampler allows a skip only after the
     first max(2, ceil(cache_start * steps)) steps, before the last max(1, ceil((1 - cache_end) * steps)), and
     for at most cache_max_hits steps in a row (engine/src/pipeline.cu:463-480, 488, 506-509). Returns x; the
@@ -78,6 +81,9 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
     v, vn = torch.empty_like(x), torch.empty_like(x)
     den, old = torch.empty_like(x), torch.empty_like(x)
     have_old = False
+    if mask is not None and init is None:
+        raise ValueError("an inpainting mask needs init")
+    xin = torch.empty_like(x) if mask is not None else x
     cfg_steps = math.ceil(cfg_until * steps - 1e-4) if negative else 0
     warm = max(2, math.ceil(cache_start * steps))
     tail = max(1, math.ceil((1.0 - cache_end) * steps))
@@ -91,7 +97,9 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
         cfg_now = i < cfg_steps
         if cache is not None:
             cache.allow = warm <= i < steps - tail and run < max_hits
-        model([v, vn], x, s * timestep_mult, cfg_now)
+        if mask is not None:
+            flow_inpaint_in(xin, x, noise, init, mask, s)
+        model([v, vn], xin, s * timestep_mult, cfg_now)
         if cache is not None:
             if cache.skipped:
                 cache.skips += 1
@@ -101,10 +109,15 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
         if cfg_now:
             cfg_combine(v, vn, cfg)
         sn = sigmas[i + 1]
-        if sampler == "euler":
+        if mask is not None:  # every sampler goes through the pinned denoised estimate
+            flow_denoised_masked(den, xin, v, init, mask, s)
+        if sampler == "euler" and mask is None:
             flow_euler_step(x, v, s, sn)
+        elif sampler == "euler":
+            flow_update(x, den, sn / s, 1.0 - sn / s)
         elif sampler == "euler_ancestral":
-            flow_denoised(den, x, v, s)
+            if mask is None:
+                flow_denoised(den, x, v, s)
             if sn == 0.0:
                 flow_update(x, den, 0.0, 1.0)
             else:
@@ -116,10 +129,11 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
                 nz = torch_randn(seed + 1 + i, x.numel()).view_as(x).to(x.device)
                 flow_update(x, nz, 1.0, renoise)
         else:
-            flow_denoised(den, x, v, s)
+            if mask is None:
+                flow_denoised(den, x, v, s)
             a, b, c = step_coef(sampler, sigmas, i, have_old)
             flow_update(x, den, a, b, old if have_old else None, c)
-        if sampler != "euler":
+        if sampler != "euler" or mask is not None:
             den, old = old, den
             have_old = True
     return x

@@ -184,6 +184,8 @@ int kiln_flow_denoised_masked(float* den, const float* xin, const float* v, cons
 /* The generic sampler step (engine/src/pipeline.cu:333-337, k_update): x = a x + b den + c old (old NULL: 0). */
 int kiln_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
                      kiln_stream_t stream);
+/* Replaces gelu() (engine/src/gpu.h:141, kernels.cu:728-733): x = x/2 (1 + erf(x / sqrt 2)) in place, fp32. */
+int kiln_gelu(float* x, size_t n, kiln_stream_t stream);
 /* Replaces cfg_combine() (engine/src/gpu.h:144, kernels.cu:1058-1062): v = vn + cfg * (v - vn), n elements. */
 int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream_t stream);
 

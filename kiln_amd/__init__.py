@@ -48,6 +48,7 @@ _SIGS = {
     "kiln_rel_l1": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "kiln_torch_randn": (_i, [_vp, ctypes.c_uint64, _sz]),
     "kiln_flow_start": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
+    "kiln_gelu": (_i, [_vp, _sz, _vp]),
     "kiln_flow_inpaint_in": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _vp]),
     "kiln_flow_denoised_masked": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _vp]),
     "kiln_flow_denoised": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
@@ -479,3 +480,9 @@ def flow_denoised_masked(den, xin, v, init, mask, sigma, stream=None):
     _check(lib().kiln_flow_denoised_masked(_ptr(den), _ptr(xin), _ptr(v), _ptr(init), _ptr(mask), sigma, mask.numel(),
                                            _stream(stream)))
     return den
+
+
+def gelu(x, stream=None):
+    """gelu (engine/src/kernels.cu:728-733): in place, fp32, erf form."""
+    _check(lib().kiln_gelu(_ptr(x), x.numel(), _stream(stream)))
+    return x

@@ -678,6 +678,12 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
     return hip_check(kiln::launch_flow_start(x, noise, init, sigma, n, (hipStream_t)stream), "flow_start launch");
 }
 
+int kiln_gelu(float* x, size_t n, kiln_stream_t stream) {
+    if (n && !x) return fail(KILN_EINVAL, "gelu: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_gelu(x, n, (hipStream_t)stream), "gelu launch");
+}
+
 int kiln_flow_inpaint_in(float* xin, const float* x, const float* noise, const float* init, const float* mask,
                          float sigma, int P, kiln_stream_t stream) {
     if (P < 0 || (P && (!xin || !x || !noise || !init || !mask))) return fail(KILN_EINVAL, "flow_inpaint_in: bad args");

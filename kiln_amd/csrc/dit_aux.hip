@@ -245,6 +245,15 @@ __global__ void k_flow_denoised_masked(float* __restrict__ den, const float* __r
     den[i] = m * d + (1.f - m) * init[i];
 }
 
+// GELU in place, fp32 (kernels.cu:728-733, the fp32 branch's MLP activation): erf form with the device erff
+__global__ void k_gelu(float* __restrict__ x, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float v = x[i];
+        x[i] = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+    }
+}
+
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
@@ -299,6 +308,10 @@ hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, h
     return hipGetLastError();
 }
 
+hipError_t launch_gelu(float* x, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_gelu, dim3(nblk(n)), dim3(256), 0, st, x, n);
+    return hipGetLastError();
+}
 hipError_t launch_flow_inpaint_in(float* xin, const float* x, const float* noise, const float* init, const float* mask,
                                   float s, int P, hipStream_t st) {
     hipLaunchKernelGGL(k_flow_inpaint_in, dim3(nblk((size_t)16 * P)), dim3(256), 0, st, xin, x, noise, init, mask, s, P);

@@ -25,7 +25,7 @@ import torch
 
 from . import (KILN_EPI_GELU16, KILN_EPI_RESID, add_gated, dit_cross_attn_x16, dit_self_attn_x16,
                kv_prepare, layernorm_mod, lib, linear16, linear16_prepare_weight, linear_f32, matvec, matvec_grouped,
-               patchify, rel_l1, rmsnorm, silu, sub, unpatchify)
+               patchify, rel_l1, rmsnorm, silu, sub, unpatchify, attention_exact, gelu, rope_half, nag_combine)
 
 HD = 128
 
@@ -96,6 +96,63 @@ def block_forward16(X, mods, blk, ws, B, T, rope, ctx, nag=None, eps=1e-6):
     layernorm_mod(ws.n16, X, mm[D:2 * D], mm[0:D], eps)
     linear16(ws.h16, ws.n16, blk.mlp1, epi=KILN_EPI_GELU16)
     linear16(X, ws.h16, blk.mlp2, epi=KILN_EPI_RESID, gate=mm[2 * D:3 * D])
+    return X
+
+
+class Block32:
+    """One block's weights for the fp32 branch (G.fp16 off, the engine's --fp32): bf16 [out, in] linear weights
+    read as fp32 (the reference's weight_f32), norm weights bf16 [128]."""
+
+    def __init__(self, sa_q, sa_k, sa_v, sa_o, ca_q, ca_o, mlp1, mlp2, sa_qn, sa_kn, ca_qn):
+        self.sa_q, self.sa_k, self.sa_v, self.sa_o = sa_q, sa_k, sa_v, sa_o
+        self.ca_q, self.ca_o, self.mlp1, self.mlp2 = ca_q, ca_o, mlp1, mlp2
+        self.sa_qn, self.sa_kn, self.ca_qn = sa_qn, sa_kn, ca_qn
+        self.D, self.F = sa_o.shape[0], mlp1.shape[0]
+
+
+def block_forward32(X, mods, blk, B, T, rope, ctx, nag=None, eps=1e-6):
+    """The fp32 branch of the block loop (engine/src/dit.cu:495-530): fp32 activations throughout, fp32 linear
+    layers (kiln_linear_f32), per-head RMSNorm + rope_half on Q/K, the exact fp32 attention per item
+    (kiln_attn_fwd_exact: attention() with G.fp16 off, kernels.cu:840-865), add_gated residuals, fp32 GELU. ctx: per item (K fp32 [L, D], V fp32 [L, D], padding
+    rows) with K already RMS-normed (Dit::cache_context); nag: None or (K, V, padding, scale, tau, alpha)."""
+    D, H = blk.D, blk.D // HD
+    R = B * T
+    dev = X.device
+    mo, mc, mm = mods[0:3 * D], mods[3 * D:6 * D], mods[6 * D:9 * D]
+    N = torch.empty(R, D, device=dev)
+    Q, K, V, A, Y = (torch.empty(R, D, device=dev) for _ in range(5))
+    rc, rs = rope
+    layernorm_mod(N, X, mo[D:2 * D], mo[0:D], eps)
+    linear_f32(Q, N, blk.sa_q)
+    linear_f32(K, N, blk.sa_k)
+    linear_f32(V, N, blk.sa_v)
+    rmsnorm(Q, Q, blk.sa_qn, rows=R * H, dim=HD, eps=eps)
+    rmsnorm(K, K, blk.sa_kn, rows=R * H, dim=HD, eps=eps)
+    for b in range(B):
+        rows = slice(b * T, (b + 1) * T)
+        rope_half(Q[rows], T, H, HD, rc, rs)
+        rope_half(K[rows], T, H, HD, rc, rs)
+        attention_exact(A[rows], Q[rows], K[rows], V[rows], T, T, H, HD)
+    linear_f32(Y, A, blk.sa_o)
+    add_gated(X, Y, mo[2 * D:3 * D])
+    layernorm_mod(N, X, mc[D:2 * D], mc[0:D], eps)
+    linear_f32(Q, N, blk.ca_q)
+    rmsnorm(Q, Q, blk.ca_qn, rows=R * H, dim=HD, eps=eps)
+    for b in range(B):
+        rows = slice(b * T, (b + 1) * T)
+        attention_exact(A[rows], Q[rows], ctx[b][0], ctx[b][1], T, ctx[b][0].shape[0], H, HD, npad=ctx[b][2])
+    if nag is not None:
+        An = torch.empty(T, D, device=dev)
+        attention_exact(An, Q[0:T], nag[0], nag[1], T, nag[0].shape[0], H, HD, npad=nag[2])
+        nag_combine(A[0:T], An, nag[3], nag[4], nag[5])
+    linear_f32(Y, A, blk.ca_o)
+    add_gated(X, Y, mc[2 * D:3 * D])
+    layernorm_mod(N, X, mm[D:2 * D], mm[0:D], eps)
+    Hid = torch.empty(R, blk.F, device=dev)
+    linear_f32(Hid, N, blk.mlp1)
+    gelu(Hid)
+    linear_f32(Y, Hid, blk.mlp2)
+    add_gated(X, Y, mm[2 * D:3 * D])
     return X
 
 

@@ -345,3 +345,55 @@ def test_dit_cross_attn_x16_fused_projection(gpu):
     d = (out.float() - ref.float()).abs()
     assert torch.isfinite(out.float()).all()
     assert d.max().item() <= 2e-3 and d.mean().item() <= 1e-4, (d.max().item(), d.mean().item())
+
+
+def test_dit_block_forward32_matches_reference(gpu):
+    """The fp32 branch of the block (engine/src/dit.cu:495-530: fp32 linears with bf16 weights, exact fp32
+    attention, fp32 GELU) against the float64 restatement without fp16 roundings: max-abs 1e-3, mean-abs 5e-5."""
+    g = torch.Generator().manual_seed(36)
+    bw = lambda o, i: _bf16w(g, o, i)  # noqa: E731
+    Wq, Wk, Wv, Wo, Wcq, Wco, W1, W2 = bw(D, D), bw(D, D), bw(D, D), bw(D, D), bw(D, D), bw(D, D), bw(F, D), bw(D, F)
+    nw = [_bf16(1 + 0.2 * torch.randn(HD, generator=g)) for _ in range(4)]
+    blk = dit.Block32(*[w.to(DEV) for w in (Wq, Wk, Wv, Wo, Wcq, Wco, W1, W2)], nw[0].to(DEV), nw[1].to(DEV),
+                      nw[2].to(DEV))
+    mods = torch.randn(9 * D, generator=g) * 0.3
+    X0 = torch.randn(B * T, D, generator=g)
+    ctx = [(_rms(torch.randn(r, D, generator=g).double(), nw[3].float().double(), H, EPS).float(),
+            torch.randn(r, D, generator=g)) for r in REALS]
+    rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
+    X = X0.to(DEV).clone()
+    dit.block_forward32(X, mods.to(DEV), blk, B, T, (rc.to(DEV), rs.to(DEV)),
+                        [(ctx[i][0].to(DEV), ctx[i][1].to(DEV), L - REALS[i]) for i in range(B)],
+                        nag=(ctx[2][0].to(DEV), ctx[2][1].to(DEV), L - REALS[2]) + NAG, eps=EPS)
+    torch.cuda.synchronize()
+    d = lambda t: t.double()  # noqa: E731
+    bf = lambda t: t.float().double()  # noqa: E731
+    x = X0.double()
+    mo, mc, mm = d(mods[:3 * D]), d(mods[3 * D:6 * D]), d(mods[6 * D:])
+
+    def ln(x, sh, sc):
+        m = x.mean(-1, keepdim=True)
+        return (x - m) / torch.sqrt(((x - m) ** 2).mean(-1, keepdim=True) + EPS) * (1 + sc) + sh
+
+    n = ln(x, mo[:D], mo[D:2 * D])
+    q, k, v = n @ bf(Wq).T, n @ bf(Wk).T, n @ bf(Wv).T
+    a = torch.empty(B * T, D, dtype=torch.float64)
+    for b in range(B):
+        r_ = slice(b * T, (b + 1) * T)
+        a[r_] = _attn(_rope(_rms(q[r_], bf(nw[0]), H, EPS), d(rc), d(rs), H),
+                      _rope(_rms(k[r_], bf(nw[1]), H, EPS), d(rc), d(rs), H), v[r_], H)
+    x = x + mo[2 * D:] * (a @ bf(Wo).T)
+    n = ln(x, mc[:D], mc[D:2 * D])
+    qc = _rms(n @ bf(Wcq).T, bf(nw[2]), H, EPS)
+    for b in range(B):
+        r_ = slice(b * T, (b + 1) * T)
+        a[r_] = _attn(qc[r_], d(ctx[b][0]), d(ctx[b][1]), H, L - REALS[b])
+    an = _attn(qc[:T], d(ctx[2][0]), d(ctx[2][1]), H, L - REALS[2])
+    a[:T] = torch.from_numpy(oracle.nag(a[:T].numpy(), an.numpy(), *NAG)).double()
+    x = x + mc[2 * D:] * (a @ bf(Wco).T)
+    n = ln(x, mm[:D], mm[D:2 * D])
+    h = n @ bf(W1).T
+    h = 0.5 * h * (1 + torch.erf(h / np.sqrt(2)))
+    x = x + mm[2 * D:] * (h @ bf(W2).T)
+    err = (X.cpu().double() - x).abs()
+    assert err.max().item() <= 1e-3 and err.mean().item() <= 5e-5, (err.max().item(), err.mean().item())

@@ -2,8 +2,10 @@
 
 The product is the C-ABI library ``kiln_amd/libkiln_attn.so`` (declared in include/kiln_attn.h).
 This module binds it with ctypes and offers thin torch-tensor wrappers named after the reference
-op layer (engine/src/gpu.h:133-156): ``attention``, ``attention16``, ``rmsnorm``, ``rope_half``,
-``nag_combine`` plus the batched/fused entry points. Tensors must live on the GPU; there is no CPU
+op layer (engine/src/gpu.h:118-156): ``attention``, ``attention16``, ``rmsnorm``, ``rope_half``,
+``nag_combine``, ``layernorm_mod``, ``add_gated``, ``linear16``, ``matvec``, ``silu``, ``gelu``, ``cfg_combine``
+plus the batched/fused entry points. ``kiln_amd.dit`` and ``kiln_amd.sampler`` compose the DiT forward and
+the flow-matching samplers from them. Tensors must live on the GPU; there is no CPU
 fallback — when the library is missing, ``lib()`` raises.
 
 Errors: a non-zero status from the library raises ``KilnError`` (the reference raises

@@ -1,6 +1,8 @@
-"""One Cosmos-Predict2 DiT block on the fp16-activation path, composed from the library's entry points.
+"""The Cosmos-Predict2 DiT forward composed from the library's entry points.
 
-Mirrors the block loop of the reference's Dit::forward_batch for G.fp16 && G.tc16 (engine/src/dit.cu:455-494):
+block_forward16 mirrors the block loop of the reference's Dit::forward_batch for G.fp16 && G.tc16
+(engine/src/dit.cu:455-494); forward16 adds the step tables, patch embedding, final layer and the first-block
+step cache (dit.cu:357-546); block_forward32 is the fp32 branch of the block (dit.cu:495-530). The fp16 block:
 
     N16 = layernorm_mod16(X; shift, scale of the self-attention modulation)
     Q, K, V = linear16(N16, sa_q / sa_k / sa_v)   one launch on [Wq; Wk; Wv] whose epilogue applies

@@ -28,6 +28,91 @@ def flow_sigmas(steps, shift=1.0, denoise=1.0):
 
 
 SAMPLERS = ("euler", "euler_ancestral", "dpmpp_2m", "res_multistep")
+SCHEDULERS = ("simple", "normal", "sgm_uniform", "karras", "exponential", "ddim_uniform", "beta", "linear_quadratic",
+              "kl_optimal")
+
+
+def _snr_shift(shift, t):
+    return t if shift == 1.0 else shift * t / (1.0 + (shift - 1.0) * t)
+
+
+def _flow_table(shift):
+    t = (np.arange(1000, dtype=np.float32) + np.float32(1)) / np.float32(1000)
+    sh = np.float32(shift)
+    return t if shift == 1.0 else (sh * t / (np.float32(1) + (sh - np.float32(1)) * t)).astype(np.float32)
+
+
+def _full_schedule(name, steps, shift):
+    """The ComfyUI schedulers over ModelSamplingDiscreteFlow(shift) (engine/src/pipeline.cu:188-262, flow space:
+    timestep(sigma) = sigma, sigma(t) = shift t / (1 + (shift - 1) t), table[i] = sigma((i + 1) / 1000))."""
+    tab = _flow_table(shift)
+    f32 = lambda v: float(np.float32(v))  # noqa: E731  (the reference stores float32)
+    smin, smax = float(tab[0]), float(tab[999])
+    if name == "simple":
+        ss = 1000.0 / steps
+        return [float(tab[999 - int(x * ss)]) for x in range(steps)] + [0.0]
+    if name in ("normal", "sgm_uniform"):
+        start, end, n, zero = smax, smin, steps, True
+        if name == "sgm_uniform":
+            ts = [start + (end - start) * i / n for i in range(n + 1)][:-1]
+        else:
+            if abs(_snr_shift(shift, end)) < 1e-5:
+                n, zero = n + 1, False
+            ts = [start if n == 1 else start + (end - start) * i / (n - 1) for i in range(n)]
+        return [f32(_snr_shift(shift, t)) for t in ts] + ([0.0] if zero else [])
+    if name == "karras":
+        a, b = smax ** (1 / 7.0), smin ** (1 / 7.0)
+        return [f32((a + (0.0 if steps == 1 else i / (steps - 1)) * (b - a)) ** 7.0) for i in range(steps)] + [0.0]
+    if name == "exponential":
+        la, lb = math.log(smax), math.log(smin)
+        return [f32(math.exp(la if steps == 1 else la + (lb - la) * i / (steps - 1))) for i in range(steps)] + [0.0]
+    if name == "ddim_uniform":
+        x, n, sig = 1, steps, []
+        if abs(float(tab[x])) < 1e-5:
+            n += 1
+        else:
+            sig.append(0.0)
+        ss = max(1000 // n, 1)
+        while x < 1000:
+            sig.append(float(tab[x]))
+            x += ss
+        return sig[::-1]
+    if name == "beta":
+        from scipy.special import betaincinv  # the Beta(0.6, 0.6) quantile (the reference's beta_ppf)
+        out, last = [], -1
+        for i in range(steps):
+            t = int(np.rint(betaincinv(0.6, 0.6, 1.0 - i / steps) * 999.0))
+            if t != last:
+                out.append(float(tab[t]))
+            last = t
+        return out + [0.0]
+    if name == "linear_quadratic":
+        if steps == 1:
+            return [1.0, 0.0]
+        thr, lin = 0.025, steps // 2
+        quad = steps - lin
+        sch = [i * thr / lin for i in range(lin)]
+        diff = lin - thr * steps
+        qc = diff / (lin * quad * quad)
+        lc = thr / lin - 2 * diff / (quad * quad)
+        cst = qc * lin * lin
+        sch += [qc * i * i + lc * i + cst for i in range(lin, steps)] + [1.0]
+        return [f32((1.0 - v) * smax) for v in sch]
+    if name == "kl_optimal":
+        return [f32(math.tan((0.0 if steps == 1 else i / (steps - 1)) * math.atan(smin) +
+                             (1 - (0.0 if steps == 1 else i / (steps - 1))) * math.atan(smax)))
+                for i in range(steps)] + [0.0]
+    raise ValueError(f"unknown scheduler {name}")
+
+
+def schedule_sigmas(name, steps, shift=1.0, denoise=1.0):
+    """schedule_sigmas (engine/src/pipeline.cu:265-277): the schedule of steps / denoise steps, last steps + 1."""
+    if denoise > 0.9999:
+        return _full_schedule(name, steps, shift)
+    if denoise <= 0:
+        return []
+    s = _full_schedule(name, int(steps / denoise), shift)
+    return s if len(s) < steps + 1 else s[len(s) - (steps + 1):]
 
 
 def step_coef(sampler, sig, i, have_old):

@@ -162,3 +162,27 @@ def test_inpainting_mask(gpu, name):
     sampler.sample_euler(model, xh, n, sig, negative=False, init=init, sampler=name, mask=m)
     torch.testing.assert_close(xh[:, :, :3], ref[:, :, :3], rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(xh[:, :, 3:], init[:, :, 3:], rtol=1e-5, atol=1e-5)
+
+
+def test_schedulers_closed_forms():
+    """Flow-space schedulers (engine/src/pipeline.cu:188-277): "simple" equals flow_sigmas; karras with rho 7 and
+    exponential are geometric/power interpolations between sigma_max = 1 and sigma_min = shift(0.001) that end in
+    0; kl_optimal is tan-linear in atan(sigma); every schedule is non-increasing and ends at 0; partial denoise
+    takes the tail of the longer schedule."""
+    import math
+    for shift in (1.0, 3.0):
+        np.testing.assert_allclose(sampler.schedule_sigmas("simple", 8, shift), sampler.flow_sigmas(8, shift), rtol=1e-7)
+        smin = shift * 0.001 / (1 + (shift - 1) * 0.001)
+        k = sampler.schedule_sigmas("karras", 5, shift)
+        assert abs(k[0] - 1.0) < 1e-6 and abs(k[4] - smin) < 1e-6 and k[5] == 0.0
+        r = [x ** (1 / 7) for x in k[:5]]
+        np.testing.assert_allclose(np.diff(r), np.diff(r)[0], rtol=1e-4)
+        e = sampler.schedule_sigmas("exponential", 5, shift)
+        np.testing.assert_allclose(np.diff(np.log(e[:5])), math.log(smin) / 4, rtol=1e-5)
+        kl = sampler.schedule_sigmas("kl_optimal", 5, shift)
+        np.testing.assert_allclose(np.diff(np.arctan(kl[:5])), (math.atan(smin) - math.atan(1.0)) / 4, rtol=1e-5)
+        for name in sampler.SCHEDULERS:
+            s = sampler.schedule_sigmas(name, 10, shift)
+            assert s[-1] == 0.0 and all(a >= b for a, b in zip(s, s[1:])), name
+        full = sampler.schedule_sigmas("karras", 20, shift)
+        np.testing.assert_allclose(sampler.schedule_sigmas("karras", 10, shift, 0.5), full[-11:], rtol=1e-7)

@@ -97,6 +97,28 @@ def test_argument_validation_without_gpu(L):
     assert L.kiln_linear16_prepare_weight(q, ctypes.c_void_p(4096 + 1024), 128, 64, 0, None) == kiln_amd.KILN_EINVAL
     assert L.kiln_linear16_prepare_weight(None, q, 128, 64, 0, None) == kiln_amd.KILN_EINVAL
     assert L.kiln_linear16_prepped(q, 128, q, 8, q, 128, 40, 0, None, 0.0, None, None, 0, None) == kiln_amd.KILN_EUNSUPPORTED
+    # fused-projection DiT sections: odd H, batch bound, workspace too small, null pointers
+    assert L.kiln_dit_self_attn_x16(q, 1, 384, q, q, q, q, 1e-6, q, q, 2, 96, 3, q, 1 << 30, None) == \
+        kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_dit_self_attn_x16(q, 1, 512, q, q, q, q, 1e-6, q, q, 5, 96, 4, q, 1 << 30, None) == \
+        kiln_amd.KILN_EUNSUPPORTED
+    assert L.kiln_dit_self_attn_x16(q, 1, 512, q, q, q, q, 1e-6, q, q, 2, 96, 4, q, 16, None) == kiln_amd.KILN_ENOMEM
+    assert L.kiln_dit_self_attn_x16(q, 1, 512, q, q, None, q, 1e-6, q, q, 2, 96, 4, q, 1 << 30, None) == \
+        kiln_amd.KILN_EINVAL
+    assert L.kiln_dit_self_attn_x16_workspace_bytes(0, 96, 4) == 0
+    assert L.kiln_dit_cross_attn_x16(q, None, 1, 512, q, q, q, 1e-6, 2, 96, 4, q, q, q, None, 0, 0, 5.0, 2.5, 0.25,
+                                     q, 16, None) == kiln_amd.KILN_ENOMEM
+    # small passes and sampler steps: null pointers and sizes
+    assert L.kiln_matvec_bf16(None, q, q, None, 4, 8, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_matvec_bf16_grouped(q, q, q, None, -1, 4, 8, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_patchify(q, q, 7, 8, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_unpatchify(q, q, 32, 8, 8, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_linear_f32(q, 4, q, 8, q, 3, 8, 8, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_flow_euler_step(q, q, 0.0, 0.5, 16, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_flow_update(None, q, None, 1.0, 0.0, 0.0, 16, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_flow_inpaint_in(q, q, q, None, q, 0.5, 16, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_rel_l1(q, q, 16, None, None) == kiln_amd.KILN_EINVAL
+    assert L.kiln_torch_randn(None, 0, 32) == kiln_amd.KILN_EINVAL
     # more batch items than one launch takes
     assert L.kiln_dit_self_attn_fused(p, 1, 2048, p, p, p, 1, 2048, None, None, 1e-6, None, None, 5, 64, 16, None, 0,
                                       None) != kiln_amd.KILN_OK

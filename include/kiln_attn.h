@@ -184,6 +184,12 @@ int kiln_flow_denoised_masked(float* den, const float* xin, const float* v, cons
 /* The generic sampler step (engine/src/pipeline.cu:333-337, k_update): x = a x + b den + c old (old NULL: 0). */
 int kiln_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
                      kiln_stream_t stream);
+/* The er_sde sampler step (engine/src/pipeline.cu:345-359, coefficients :361-391): x = a x + b den; from stage 2
+ * + c2 dd with dd = (den - old) * inv2 (stored into oldd); at stage 3 + c3 (dd - oldd_prev) * inv3; + cn noise
+ * (noise NULL: none). */
+int kiln_flow_ersde_step(float* x, const float* den, const float* old, float* oldd, const float* noise, float a,
+                         float b, float c2, float inv2, float c3, float inv3, float cn, int stage, size_t n,
+                         kiln_stream_t stream);
 /* Replaces gelu() (engine/src/gpu.h:141, kernels.cu:728-733): x = x/2 (1 + erf(x / sqrt 2)) in place, fp32. */
 int kiln_gelu(float* x, size_t n, kiln_stream_t stream);
 /* Replaces cfg_combine() (engine/src/gpu.h:144, kernels.cu:1058-1062): v = vn + cfg * (v - vn), n elements. */

@@ -51,6 +51,7 @@ _SIGS = {
     "kiln_torch_randn": (_i, [_vp, ctypes.c_uint64, _sz]),
     "kiln_flow_start": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
     "kiln_gelu": (_i, [_vp, _sz, _vp]),
+    "kiln_flow_ersde_step": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _f, _f, _f, _f, _f, _f, _i, _sz, _vp]),
     "kiln_flow_inpaint_in": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _vp]),
     "kiln_flow_denoised_masked": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _vp]),
     "kiln_flow_denoised": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
@@ -487,4 +488,12 @@ def flow_denoised_masked(den, xin, v, init, mask, sigma, stream=None):
 def gelu(x, stream=None):
     """gelu (engine/src/kernels.cu:728-733): in place, fp32, erf form."""
     _check(lib().kiln_gelu(_ptr(x), x.numel(), _stream(stream)))
+    return x
+
+
+def flow_ersde_step(x, den, old, oldd, noise, c, stream=None):
+    """k_ersde (engine/src/pipeline.cu:345-359) with the coefficients c = (a, b, c2, inv2, c3, inv3, cn, stage)."""
+    a, b, c2, inv2, c3, inv3, cn, stage = c
+    _check(lib().kiln_flow_ersde_step(_ptr(x), _ptr(den), _ptr(old), _ptr(oldd), _ptr(noise), a, b, c2, inv2, c3, inv3,
+                                      cn, stage, x.numel(), _stream(stream)))
     return x

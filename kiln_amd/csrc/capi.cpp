@@ -678,6 +678,17 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
     return hip_check(kiln::launch_flow_start(x, noise, init, sigma, n, (hipStream_t)stream), "flow_start launch");
 }
 
+int kiln_flow_ersde_step(float* x, const float* den, const float* old, float* oldd, const float* noise, float a,
+                         float b, float c2, float inv2, float c3, float inv3, float cn, int stage, size_t n,
+                         kiln_stream_t stream) {
+    if (stage < 1 || stage > 3) return fail(KILN_EINVAL, "flow_ersde_step: stage %d", stage);
+    if (n && (!x || !den || (stage >= 2 && (!old || !oldd)))) return fail(KILN_EINVAL, "flow_ersde_step: null pointer");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_flow_ersde(x, den, old, oldd, noise, a, b, c2, inv2, c3, inv3, cn, stage, n,
+                                             (hipStream_t)stream),
+                     "flow_ersde launch");
+}
+
 int kiln_gelu(float* x, size_t n, kiln_stream_t stream) {
     if (n && !x) return fail(KILN_EINVAL, "gelu: null pointer");
     if (!n) return KILN_OK;

@@ -254,6 +254,25 @@ __global__ void k_gelu(float* __restrict__ x, size_t n) {
     }
 }
 
+// er_sde step (pipeline.cu:345-359): x <- a x + b den (+ c2 dd (+ c3 (dd - oldd) inv3) from stage 2, with
+// dd = (den - old) inv2, which is kept in oldd for the next step) (+ cn noise)
+__global__ void k_flow_ersde(float* __restrict__ x, const float* __restrict__ den, const float* __restrict__ old,
+                             float* __restrict__ oldd, const float* __restrict__ noise, float a, float b, float c2,
+                             float inv2, float c3, float inv3, float cn, int stage, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float d = den[i];
+    float v = a * x[i] + b * d;
+    if (stage >= 2) {
+        const float dd = (d - old[i]) * inv2;
+        v += c2 * dd;
+        if (stage >= 3) v += c3 * (dd - oldd[i]) * inv3;
+        oldd[i] = dd;
+    }
+    if (noise) v += cn * noise[i];
+    x[i] = v;
+}
+
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
@@ -308,6 +327,13 @@ hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, h
     return hipGetLastError();
 }
 
+hipError_t launch_flow_ersde(float* x, const float* den, const float* old, float* oldd, const float* noise, float a,
+                             float b, float c2, float inv2, float c3, float inv3, float cn, int stage, size_t n,
+                             hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_ersde, dim3(nblk(n)), dim3(256), 0, st, x, den, old, oldd, noise, a, b, c2, inv2, c3, inv3,
+                       cn, stage, n);
+    return hipGetLastError();
+}
 hipError_t launch_gelu(float* x, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(k_gelu, dim3(nblk(n)), dim3(256), 0, st, x, n);
     return hipGetLastError();

@@ -102,6 +102,9 @@ hipError_t launch_sub(float* y, const float* a, const float* b, size_t n, hipStr
 hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, hipStream_t st);
 hipError_t launch_flow_start(float* x, const float* noise, const float* init, float s, size_t n, hipStream_t st);
 hipError_t launch_gelu(float* x, size_t n, hipStream_t st);
+hipError_t launch_flow_ersde(float* x, const float* den, const float* old, float* oldd, const float* noise, float a,
+                             float b, float c2, float inv2, float c3, float inv3, float cn, int stage, size_t n,
+                             hipStream_t st);
 hipError_t launch_flow_inpaint_in(float* xin, const float* x, const float* noise, const float* init, const float* mask,
                                   float s, int P, hipStream_t st);
 hipError_t launch_flow_denoised_masked(float* den, const float* xin, const float* v, const float* init,

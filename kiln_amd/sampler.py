@@ -10,8 +10,8 @@ import math
 
 import numpy as np
 
-from . import (cfg_combine, flow_denoised, flow_denoised_masked, flow_euler_step, flow_inpaint_in, flow_start,
-               flow_update, torch_randn)
+from . import (cfg_combine, flow_denoised, flow_denoised_masked, flow_ersde_step, flow_euler_step, flow_inpaint_in,
+               flow_start, flow_update, torch_randn)
 
 
 def flow_sigmas(steps, shift=1.0, denoise=1.0):
@@ -27,7 +27,7 @@ def flow_sigmas(steps, shift=1.0, denoise=1.0):
     return s[len(s) - (steps + 1):]
 
 
-SAMPLERS = ("euler", "euler_ancestral", "dpmpp_2m", "res_multistep")
+SAMPLERS = ("euler", "euler_ancestral", "dpmpp_2m", "res_multistep", "er_sde")
 SCHEDULERS = ("simple", "normal", "sgm_uniform", "karras", "exponential", "ddim_uniform", "beta", "linear_quadratic",
               "kl_optimal")
 
@@ -133,6 +133,41 @@ def step_coef(sampler, sig, i, have_old):
     return math.exp(-h), h * (phi1 - phi2 / c2), h * (phi2 / c2)
 
 
+def ersde_coef(sig, i):
+    """Coefficients of the er_sde step from sigma_i to sigma_{i+1} (engine/src/pipeline.cu:361-391): lambda =
+    sigma / (1 - sigma), noise scaler f(l) = l (exp(l^0.3) + 10), the integrals of 1/f and (l - l_i)/f over
+    [l_{i+1}, l_i] by a 200-point left sum; stage min(3, i + 1). Returns (a, b, c2, inv2, c3, inv3, cn, stage)."""
+    def lam(k):
+        return sig[k] / (1.0 - sig[k])
+
+    def f(l):
+        return l * (math.exp(l ** 0.3) + 10.0)
+
+    ls, lt = lam(i), lam(i + 1)
+    as_, at = sig[i] / ls, sig[i + 1] / lt
+    r, ra = f(lt) / f(ls), at / as_
+    stage = min(3, i + 1)
+    a, b, c2, inv2, c3, inv3 = ra * r, at * (1.0 - r), 0.0, 0.0, 0.0, 0.0
+    if stage >= 2:
+        dt = lt - ls
+        step = -dt / 200.0
+        S = Su = 0.0
+        for k in range(200):
+            lp = lt + k * step
+            fp = f(lp)
+            S += 1.0 / fp
+            Su += (lp - ls) / fp
+        S *= step
+        Su *= step
+        c2 = at * (dt + S * f(lt))
+        inv2 = 1.0 / (ls - lam(i - 1))
+        if stage >= 3:
+            c3 = at * (dt * dt / 2.0 + Su * f(lt))
+            inv3 = 2.0 / (ls - lam(i - 2))
+    cn = at * math.sqrt(max(0.0, lt * lt - ls * ls * r * r))
+    return a, b, c2, inv2, c3, inv3, cn, stage
+
+
 def initial_noise(seed, shape, device):
     """The sampler's noise (engine/src/pipeline.cu:428-429): torch_randn(seed, n) on the host, then to the device."""
     from . import torch_randn
@@ -148,7 +183,8 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
     negative context into outs[1]; x [16, Hl, Wl] fp32 (overwritten with the result), noise like x;
     negative: whether a negative context exists (CFG runs for the first ceil(cfg_until * steps) steps).
     sampler: "euler" (k_euler_step's arithmetic), "euler_ancestral" (the RF ancestral step with eta 1, fresh
-    noise torch_randn(seed + 1 + i) per step, pipeline.cu:514-529), "dpmpp_2m" or "res_multistep" (step_coef).
+    noise torch_randn(seed + 1 + i) per step, pipeline.cu:514-529), "dpmpp_2m" or "res_multistep" (step_coef),
+    "er_sde" (ersde_coef, up to third order, same per-step noise, pipeline.cu:538-547).
     mask: inpainting mask [Hl, Wl] (1 = regenerate) with init: the model sees the init re-noised to each sigma
     outside the mask and the denoised estimate is pinned to the init there (pipeline.cu:309-324, 485, 512).
     cache: a kiln_amd.dit.StepCache the model's forward uses, or None; the sampler allows a skip only after the
@@ -169,6 +205,11 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
     if mask is not None and init is None:
         raise ValueError("an inpainting mask needs init")
     xin = torch.empty_like(x) if mask is not None else x
+    if sampler == "er_sde":
+        oldd = torch.empty_like(x)
+        sigmas = list(sigmas)
+        if sigmas[0] >= 1.0:
+            sigmas[0] = 1.0 - 1e-4  # lambda = sigma / (1 - sigma) needs sigma < 1 (pipeline.cu:482)
     cfg_steps = math.ceil(cfg_until * steps - 1e-4) if negative else 0
     warm = max(2, math.ceil(cache_start * steps))
     tail = max(1, math.ceil((1.0 - cache_end) * steps))
@@ -200,6 +241,14 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
             flow_euler_step(x, v, s, sn)
         elif sampler == "euler":
             flow_update(x, den, sn / s, 1.0 - sn / s)
+        elif sampler == "er_sde":
+            if mask is None:
+                flow_denoised(den, x, v, s)
+            if sn == 0.0:
+                flow_update(x, den, 0.0, 1.0)
+            else:
+                nz = torch_randn(seed + 1 + i, x.numel()).view_as(x).to(x.device)
+                flow_ersde_step(x, den, old, oldd, nz, ersde_coef(sigmas, i))
         elif sampler == "euler_ancestral":
             if mask is None:
                 flow_denoised(den, x, v, s)

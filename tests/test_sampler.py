@@ -186,3 +186,55 @@ def test_schedulers_closed_forms():
             assert s[-1] == 0.0 and all(a >= b for a, b in zip(s, s[1:])), name
         full = sampler.schedule_sigmas("karras", 20, shift)
         np.testing.assert_allclose(sampler.schedule_sigmas("karras", 10, shift, 0.5), full[-11:], rtol=1e-7)
+
+
+def test_ersde_coefficients_keep_the_data_point():
+    """er_sde (engine/src/pipeline.cu:361-391) is exact for a sample that is all data: with x = (1 - s) x0 and
+    den = x0 the noise-free part a x + b den equals (1 - s') x0, i.e. a (1 - s) + b = 1 - s'; the noise scale is
+    real and non-negative; the stage grows 1, 2, 3."""
+    sig = sampler.flow_sigmas(8, 3.0)
+    sig[0] = 1.0 - 1e-4
+    for i in range(7):
+        a, b, c2, inv2, c3, inv3, cn, stage = sampler.ersde_coef(sig, i)
+        assert abs(a * (1 - sig[i]) + b - (1 - sig[i + 1])) < 1e-9
+        assert cn >= 0 and stage == min(3, i + 1)
+
+
+@pytest.mark.gpu
+def test_ersde_kernel_stages(gpu):
+    """kiln_flow_ersde_step against a float64 statement of k_ersde for stages 1-3 (oldd written at stage >= 2)."""
+    g = torch.Generator().manual_seed(13)
+    x, den, old, oldd, nz = (torch.randn(1000, generator=g) for _ in range(5))
+    for stage in (1, 2, 3):
+        c = (0.7, 0.2, -0.3, -0.5, 0.1, -0.2, 0.4, stage)
+        xd, od = x.to(DEV), oldd.to(DEV)
+        kiln_amd.flow_ersde_step(xd, den.to(DEV), old.to(DEV), od, nz.to(DEV), c)
+        v = 0.7 * x.double() + 0.2 * den.double()
+        dd = (den.double() - old.double()) * -0.5
+        if stage >= 2:
+            v = v + -0.3 * dd
+        if stage >= 3:
+            v = v + 0.1 * (dd - oldd.double()) * -0.2
+        v = v + 0.4 * nz.double()
+        np.testing.assert_allclose(xd.cpu().double().numpy(), v.numpy(), rtol=1e-5, atol=1e-6)
+        if stage >= 2:
+            np.testing.assert_allclose(od.cpu().double().numpy(), dd.numpy(), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.gpu
+def test_ersde_sampling_runs_deterministically(gpu):
+    """A 6-step er_sde run (stages 1-3 and the final step to sigma 0) is finite and repeats bit for bit with the
+    same seed (its noise is the library's torch_randn(seed + 1 + i))."""
+    g = torch.Generator().manual_seed(14)
+    x0, n = torch.randn(16, 4, 6, generator=g).to(DEV), torch.randn(16, 4, 6, generator=g).to(DEV)
+
+    def model(outs, xx, t, cfg_now):
+        outs[0].copy_(n - x0)
+
+    sig = sampler.flow_sigmas(6, 3.0)
+    runs = []
+    for _ in range(2):
+        x = torch.empty_like(x0)
+        sampler.sample_euler(model, x, n, sig, negative=False, sampler="er_sde", seed=9)
+        runs.append(x.cpu())
+    assert torch.isfinite(runs[0]).all() and torch.equal(runs[0], runs[1])

@@ -239,18 +239,16 @@ def linear16_cases(torch, kiln_amd, tm, dev, steps, warmup):
     return lin, blk_us, blk_fl
 
 
-def run_probe():
-    """Runs kiln_amd/probe/mfma_mix (built by kiln_amd/build.py) in a child process; {} if it is not built."""
-    import subprocess
-    exe = os.path.join(ROOT, "kiln_amd", "probe", "mfma_mix")
-    if not os.path.exists(exe):
-        log("bench.py: kiln_amd/probe/mfma_mix is not built; no sustained-throughput probe")
-        return {}
-    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
-    if r.returncode != 0:
-        log(f"bench.py: probe failed ({r.returncode}): {r.stderr.strip()}")
-        return {}
-    return json.loads(r.stdout.strip().splitlines()[-1])
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(case, target_s=10.0):
@@ -285,6 +283,7 @@ def cpu_baseline(case, target_s=10.0):
     flop = 4.0 * rows * H * T * D
     what = (f"config 4, {items} of {B} CFG items in full" if R == T else f"config 4 item 0: {R} of {T} query rows")
     return dict(value=round(flop / dt / 1e12, 5), unit="TFLOP/s", cores=oracle.num_threads(), kind="port",
+                nproc=os.cpu_count(), cpu_model=cpu_model(),
                 sample=f"{what} x {H} heads x {T} keys (+ QK-RMSNorm, RoPE), fp32 two-pass reference attention, "
                        f"{dt:.1f} s")
 
@@ -301,8 +300,6 @@ def main():
                     help="run only the DiT-shape linear16 cases (for rocprofv3 runs)")
     ap.add_argument("--forward-only", action="store_true",
                     help="run only the config-5 DiT forward of the CFG pair (for rocprofv3 runs)")
-    ap.add_argument("--probe", action="store_true",
-                    help="only run the sustained matrix-core probe (kiln_amd/probe/mfma_mix) and print its JSON")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="MIB",
                     help="copy a MIB-sized device buffer --steps times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -310,10 +307,6 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path has no "
               f"collective and shards by head with no communication, so run with --gpus 1.", file=sys.stderr)
         return 2
-
-    if args.probe:
-        print(json.dumps(run_probe()), flush=True)
-        return 0
 
     import torch
     import kiln_amd
@@ -463,9 +456,6 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("traffic_bytes")
 
-    probe = run_probe()
-    log(f"sustained matrix-core probe: {probe}")
-
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg4)
@@ -526,13 +516,6 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(tf4_main / PEAK_TFLOPS, 4),
             "traffic": traffic,
-            # what the chip sustains under a long matrix-core load (kiln_amd/probe/mfma_mix): pure
-            # v_mfma_f32_32x32x16_f16 on random fp16 data, and the same with the key loop's per-MFMA side
-            # work (1 KB LDS operand read, one exp2, two FMAs); the spec peak assumes 2.4 GHz
-            "sustained_mfma_tflops": probe.get("mfma32_tflops"),
-            "sustained_mix_tflops": probe.get("mix32_tflops"),
-            "frac_of_sustained_mfma": (round(tf4_main / probe["mfma32_tflops"], 4)
-                                       if probe.get("mfma32_tflops") else None),
         },
         "cpu_baseline": cpu,
     }

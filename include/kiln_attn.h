@@ -46,6 +46,26 @@ const char* kiln_attn_last_error(void);
 int kiln_attn_device_arch(int dev, char* buf, int buflen);
 
 /* ------------------------------------------------------------------------------------------
+ * Workspace of the entry points that take none (the drop-ins kiln_attn_fwd_f32out / _f16out and any
+ * call passing workspace = NULL): the fp16 K/V tiles and key-split partials. The reference's flash
+ * paths allocate nothing per call (they use the engine's arena, engine/src/gpu.h:51-59,
+ * kernels.cu:293-301); to get the same, set the workspace up once per device:
+ *   - kiln_attn_set_workspace(ptr, bytes): bind a caller-owned buffer (e.g. an arena slice,
+ *     256-byte aligned) to the current device; NULL unbinds;
+ *   - kiln_attn_workspace_reserve(bytes): the library allocates it now (synchronizes the device).
+ * After either, no call allocates or synchronizes (so calls can be captured into a HIP graph);
+ * a call needing more than the buffer returns KILN_ENOMEM. Without either, the first call that
+ * needs more allocates (grow-only, outgrown buffers kept until kiln_attn_workspace_release).
+ * Calls sharing one device's workspace must be ordered on one stream.
+ * ------------------------------------------------------------------------------------------ */
+/* Bytes one drop-in call (kiln_attn_fwd_f32out / _f16out, flash path) of this shape needs. */
+size_t kiln_attn_dropin_workspace_bytes(int Tq, int Tk, int H);
+int kiln_attn_workspace_reserve(size_t bytes);
+int kiln_attn_set_workspace(void* ptr, size_t bytes);
+/* Synchronizes the current device and frees the library-owned buffers (a bound buffer stays bound). */
+int kiln_attn_workspace_release(void);
+
+/* ------------------------------------------------------------------------------------------
  * Drop-in replacements of the reference op layer
  * ------------------------------------------------------------------------------------------ */
 
@@ -53,7 +73,7 @@ int kiln_attn_device_arch(int dev, char* buf, int buflen);
  * fp32 Q/K/V/out. Dh == 128 and !causal run the fp16-MFMA flash kernel (the reference's
  * tfa::k_flash<float> path, engine/src/tcflash.cuh:20-157); any other Dh (<= 256) or causal runs
  * the exact fp32 kernel (the reference's cuBLAS fallback semantics, kernels.cu:809-866).
- * Uses a library-owned, grow-only device workspace for the fp16 K/V tiles. */
+ * Uses the device's workspace (above) for the fp16 K/V tiles. */
 int kiln_attn_fwd_f32out(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                          int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream);
 
@@ -172,6 +192,9 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
 /* One Euler step of the velocity v without a mask (engine/src/pipeline.cu:318-331, k_denoised then
  * k_euler_step): den = x - v * sigma; x = x + (x - den) / sigma * (sigma_next - sigma). sigma > 0. */
 int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next, size_t n, kiln_stream_t stream);
+/* k_euler_step (engine/src/pipeline.cu:326-331) on a given denoised estimate (the masked Euler path):
+ * x = x + (x - den) / sigma * (sigma_next - sigma). sigma > 0. */
+int kiln_flow_euler_den(float* x, const float* den, float sigma, float sigma_next, size_t n, kiln_stream_t stream);
 /* The sampler's denoised estimate without a mask (engine/src/pipeline.cu:318-324): den = x - v * sigma. */
 int kiln_flow_denoised(float* den, const float* x, const float* v, float sigma, size_t n, kiln_stream_t stream);
 /* Inpainting (engine/src/pipeline.cu:309-324), latents [16, P] and mask [P]: the model input

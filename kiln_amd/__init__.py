@@ -57,6 +57,11 @@ _SIGS = {
     "kiln_flow_denoised": (_i, [_vp, _vp, _vp, _f, _sz, _vp]),
     "kiln_flow_update": (_i, [_vp, _vp, _vp, _f, _f, _f, _sz, _vp]),
     "kiln_flow_euler_step": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
+    "kiln_flow_euler_den": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
+    "kiln_attn_dropin_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kiln_attn_workspace_reserve": (_i, [_sz]),
+    "kiln_attn_set_workspace": (_i, [_vp, _sz]),
+    "kiln_attn_workspace_release": (_i, []),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "kiln_linear16_prepped_weight_bytes": (_sz, [_i, _i]),
     "kiln_linear16_prepare_weight": (_i, [_vp, _vp, _i, _i, _i, _vp]),
@@ -146,6 +151,24 @@ def _bf16_bits(w):
     if w.dtype != torch.bfloat16 or not w.is_contiguous() or w.numel() < 128:
         raise TypeError("norm weights must be a contiguous bf16 tensor of >= 128 elements")
     return _ptr(w)
+
+
+def _f32s(n, *ts):
+    """Every tensor in ts (None skipped) is float32, contiguous, on one device and holds n elements; the kernels
+    index n elements of each, so a mismatch would read or write out of bounds."""
+    import torch
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"expected a contiguous float32 tensor, got {t.dtype} (contiguous={t.is_contiguous()})")
+        if t.numel() != n:
+            raise ValueError(f"expected {n} elements, got {t.numel()} (shape {tuple(t.shape)})")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
 
 
 def _ld(t):
@@ -389,24 +412,36 @@ def linear_f32(y, x, w_bf16, stream=None):
 
 def cfg_combine(v, vn, cfg, stream=None):
     """cfg_combine (engine/src/kernels.cu:1058-1062): v = vn + cfg (v - vn)."""
+    _f32s(v.numel(), v, vn)
     _check(lib().kiln_cfg_combine(_ptr(v), _ptr(vn), cfg, v.numel(), _stream(stream)))
     return v
 
 
 def flow_start(x, noise, sigma, init=None, stream=None):
     """k_start (engine/src/pipeline.cu:304-307): x = sigma noise + (1 - sigma) init."""
+    _f32s(x.numel(), x, noise, init)
     _check(lib().kiln_flow_start(_ptr(x), _ptr(noise), _ptr(init), sigma, x.numel(), _stream(stream)))
     return x
 
 
 def flow_euler_step(x, v, sigma, sigma_next, stream=None):
     """k_denoised + k_euler_step (engine/src/pipeline.cu:318-331) without a mask, in place on x."""
+    _f32s(x.numel(), x, v)
     _check(lib().kiln_flow_euler_step(_ptr(x), _ptr(v), sigma, sigma_next, x.numel(), _stream(stream)))
+    return x
+
+
+def flow_euler_den(x, den, sigma, sigma_next, stream=None):
+    """k_euler_step (engine/src/pipeline.cu:326-331) on a given denoised estimate (the masked path):
+    x = x + (x - den) / sigma * (sigma_next - sigma), in place."""
+    _f32s(x.numel(), x, den)
+    _check(lib().kiln_flow_euler_den(_ptr(x), _ptr(den), sigma, sigma_next, x.numel(), _stream(stream)))
     return x
 
 
 def sub(y, a, b, stream=None):
     """k_sub (engine/src/dit.cu:337-340): y = a - b."""
+    _f32s(a.numel(), y, a, b)
     _check(lib().kiln_sub(_ptr(y), _ptr(a), _ptr(b), a.numel(), _stream(stream)))
     return y
 
@@ -461,18 +496,22 @@ def dit_cross_attn_x16(out, x16, wq, B, T, H, kvps, Lks, npads, q_norm_w, eps=1e
 
 def flow_denoised(den, x, v, sigma, stream=None):
     """k_denoised without a mask (engine/src/pipeline.cu:318-324): den = x - v sigma."""
+    _f32s(x.numel(), den, x, v)
     _check(lib().kiln_flow_denoised(_ptr(den), _ptr(x), _ptr(v), sigma, x.numel(), _stream(stream)))
     return den
 
 
 def flow_update(x, den, a, b, old=None, c=0.0, stream=None):
     """k_update (engine/src/pipeline.cu:333-337): x = a x + b den + c old."""
+    _f32s(x.numel(), x, den, old)
     _check(lib().kiln_flow_update(_ptr(x), _ptr(den), _ptr(old), a, b, c, x.numel(), _stream(stream)))
     return x
 
 
 def flow_inpaint_in(xin, x, noise, init, mask, sigma, stream=None):
     """k_inpaint_in (engine/src/pipeline.cu:309-315): latents [16, ...], mask [P] per pixel."""
+    _f32s(mask.numel(), mask)
+    _f32s(16 * mask.numel(), xin, x, noise, init)
     _check(lib().kiln_flow_inpaint_in(_ptr(xin), _ptr(x), _ptr(noise), _ptr(init), _ptr(mask), sigma, mask.numel(),
                                       _stream(stream)))
     return xin
@@ -480,6 +519,8 @@ def flow_inpaint_in(xin, x, noise, init, mask, sigma, stream=None):
 
 def flow_denoised_masked(den, xin, v, init, mask, sigma, stream=None):
     """k_denoised with a mask (engine/src/pipeline.cu:317-324): pinned to init where the mask is 0."""
+    _f32s(mask.numel(), mask)
+    _f32s(16 * mask.numel(), den, xin, v, init)
     _check(lib().kiln_flow_denoised_masked(_ptr(den), _ptr(xin), _ptr(v), _ptr(init), _ptr(mask), sigma, mask.numel(),
                                            _stream(stream)))
     return den
@@ -487,6 +528,7 @@ def flow_denoised_masked(den, xin, v, init, mask, sigma, stream=None):
 
 def gelu(x, stream=None):
     """gelu (engine/src/kernels.cu:728-733): in place, fp32, erf form."""
+    _f32s(x.numel(), x)
     _check(lib().kiln_gelu(_ptr(x), x.numel(), _stream(stream)))
     return x
 
@@ -494,6 +536,7 @@ def gelu(x, stream=None):
 def flow_ersde_step(x, den, old, oldd, noise, c, stream=None):
     """k_ersde (engine/src/pipeline.cu:345-359) with the coefficients c = (a, b, c2, inv2, c3, inv3, cn, stage)."""
     a, b, c2, inv2, c3, inv3, cn, stage = c
+    _f32s(x.numel(), x, den, old, oldd, noise)
     _check(lib().kiln_flow_ersde_step(_ptr(x), _ptr(den), _ptr(old), _ptr(oldd), _ptr(noise), a, b, c2, inv2, c3, inv3,
                                       cn, stage, x.numel(), _stream(stream)))
     return x

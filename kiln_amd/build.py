@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkiln_attn.so")
-SOURCES = ["attn_fwd.hip", "elementwise.hip", "gemm16.hip", "dit_aux.hip", "host_rng.cpp", "capi.cpp"]
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -48,13 +48,6 @@ def build(verbose=False):
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)
-    # sustained matrix-core probe (a measurement aid for bench.py --probe, not part of the library)
-    probe = os.path.join(HERE, "probe", "mfma_mix")
-    cmd = [HIPCC, *FLAGS, "-Wno-unused-result", os.path.join(HERE, "probe", "mfma_mix.hip"), "-o", probe + ".tmp"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"probe build failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(probe + ".tmp", probe)
     return LIB
 
 

@@ -223,8 +223,8 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 
 // ------------------------------------------------------------------------------------------------
 // The kernel. A wave owns QB query blocks of 32 rows, a workgroup NW waves (BM = NW * QB * 32 = 128
-// rows), two workgroups per CU. QB = 1 (two waves per SIMD) is the default; QB = 2 (64 rows per wave, one
-// wave per SIMD, operand reads and DMA shared by both blocks) builds and is correct but measured slower.
+// rows), two workgroups per CU. QB = 1: two waves per SIMD (64 rows per wave at one wave per SIMD measured
+// slower). NS = 5 ring stages.
 //
 // Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB) through an NS-stage LDS ring filled by
 // direct global->LDS DMA (buffer_load_dwordx4 ... lds: no staging registers, no ds_write), NS-2 half
@@ -238,39 +238,18 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 //   PV_j MFMAs interleaved with max(S_{j+1})
 // Every read of a stage completes before the barrier that precedes its refill.
 // ------------------------------------------------------------------------------------------------
-#ifndef KILN_NS
-#define KILN_NS 5
-#endif
-#ifndef KILN_QB
-#define KILN_QB 1
-#endif
-#ifndef KILN_NW
-#define KILN_NW (4 / KILN_QB)
-#endif
-#ifndef KILN_FENCES
-#define KILN_FENCES 1
-#endif
-#if KILN_FENCES
+// a scheduling fence: keeps the phases of a step in the order written and bounds the live registers
 #define KILN_FENCE() __builtin_amdgcn_sched_barrier(0)
-#else
-#define KILN_FENCE() ((void)0)
-#endif
 typedef __attribute__((address_space(3))) half8 lds_half8;
-constexpr int QB = KILN_QB, NW = KILN_NW, NTHR = NW * 64, BM = NW * QB * 32, NS = KILN_NS;
+constexpr int QB = 1, NW = 4, NTHR = NW * 64, BM = NW * QB * 32, NS = 5;
 constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
 constexpr int PART_FLOATS = BM * HD + 2 * BM;      // one key range's partial result of a query tile
 static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
 static_assert(NW * QB == 4, "two workgroups of four 32-row blocks per CU");
 
-#if KILN_CLOCK
-__device__ long long g_clk[16384][2];  // per workgroup: shader cycles, 100 MHz ticks (debug builds only)
-#endif
 
 template <typename InT, typename OutT, bool QNORM, bool ROPE>
 __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {  // 2nd: waves per SIMD
-#if KILN_CLOCK
-    const long long clk0 = __builtin_amdgcn_s_memtime(), rt0 = __builtin_amdgcn_s_memrealtime();
-#endif
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];  // NS x 16 KB
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -549,12 +528,6 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
             epilogue<OutT>(p, J, row[b], qin[b], W.h, hh, m[b], l[b], o[b]);
         }
     }
-#if KILN_CLOCK
-    if (tid == 0 && blockIdx.x < 16384) {
-        g_clk[blockIdx.x][0] = __builtin_amdgcn_s_memtime() - clk0;
-        g_clk[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime() - rt0;
-    }
-#endif
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -861,9 +834,3 @@ hipError_t launch_kv_prep(const KVPrepJob* jobs, int njobs, DT in, int Tk, int H
 
 }  // namespace kiln
 
-#if KILN_CLOCK
-extern "C" int kiln_debug_clock(long long* host, int n) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kiln::g_clk), sizeof(long long) * 2 * n);
-}
-
-#endif

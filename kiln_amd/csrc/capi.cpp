@@ -11,11 +11,12 @@
 
 #include "../../include/kiln_attn.h"
 #include "common.hpp"
+#include "capi_util.hpp"
 #include "internal.hpp"
 
 using kiln::DT;
 
-namespace {
+namespace kiln::capi {
 
 thread_local char g_err[512] = "";
 
@@ -33,42 +34,64 @@ int hip_check(hipError_t e, const char* what) {
     return fail(KILN_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Library-owned grow-only device workspace, one per device (used when the caller passes none).
-// Calls are stream-ordered on the caller's stream; concurrent calls on different streams of one
+// Per-device workspace of the entry points that take none (the drop-ins among them): the prepared K/V tiles
+// and key-split partials. Three modes per device:
+//   * bound: kiln_attn_set_workspace gave a caller-owned buffer (e.g. a slice of the engine's arena);
+//   * reserved: kiln_attn_workspace_reserve allocated one at set-up;
+//   * neither: the first call that needs more allocates (grow-only; the outgrown buffer is kept, not freed, so
+//     nothing has to wait for earlier stream-ordered users of it; kiln_attn_workspace_release frees them).
+// Once bound or reserved, no call allocates or synchronizes: one whose need exceeds the buffer fails with
+// KILN_ENOMEM. Calls are stream-ordered on the caller's stream; concurrent calls on different streams of one
 // device must pass their own workspaces.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
+    bool fixed = false;      // bound or reserved: never grows
+    bool owned = false;      // ptr was allocated by the library
+    std::vector<void*> old;  // outgrown library buffers
 };
 std::mutex g_ws_mu;
 std::vector<Workspace> g_ws;
 
+int current_device(int* dev) {
+    hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return hip_check(e, "hipGetDevice");
+    return KILN_OK;
+}
+
+Workspace& ws_of(int dev) {
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
+    return g_ws[dev];
+}
+
 int get_workspace(size_t need, void** out) {
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_check(e, "hipGetDevice");
+    if (int r = current_device(&dev)) return r;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
-    Workspace& w = g_ws[dev];
+    Workspace& w = ws_of(dev);
     if (w.bytes < need) {
-        if (w.ptr) {
-            // earlier stream-ordered users of the old buffer must finish before it is released
-            e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_check(e, "hipDeviceSynchronize");
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-        }
-        size_t sz = need + need / 4;
-        e = hipMalloc(&w.ptr, sz);
-        if (e != hipSuccess) {
-            w.ptr = nullptr;
-            return fail(KILN_ENOMEM, "workspace hipMalloc(%zu): %s", sz, hipGetErrorString(e));
-        }
+        if (w.fixed)
+            return fail(KILN_ENOMEM, "workspace of device %d holds %zu bytes, this call needs %zu (set up with "
+                        "kiln_attn_workspace_reserve / kiln_attn_set_workspace)", dev, w.bytes, need);
+        const size_t sz = need + need / 4;
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, sz);
+        if (e != hipSuccess) return fail(KILN_ENOMEM, "workspace hipMalloc(%zu): %s", sz, hipGetErrorString(e));
+        if (w.ptr) w.old.push_back(w.ptr);
+        w.ptr = p;
         w.bytes = sz;
+        w.owned = true;
     }
     *out = w.ptr;
     return KILN_OK;
+}
+
+// frees every library-owned buffer of device dev (the caller has synchronized)
+void drop_owned(Workspace& w) {
+    for (void* p : w.old) (void)hipFree(p);
+    w.old.clear();
+    if (w.owned && w.ptr) (void)hipFree(w.ptr);
+    w = Workspace{};
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -92,8 +115,7 @@ int check_common(int Tq, int Tk, int H, int npad) {
 
 // output when there are no real keys but npad zero keys: softmax mass all on zero values -> 0
 int zero_rows(void* out, int ldo, size_t esz, int Tq, int H, int Dh, hipStream_t s) {
-    hipError_t e = hipMemset2DAsync(out, (size_t)ldo * esz, 0, (size_t)H * Dh * esz, Tq, s);
-    return hip_check(e, "hipMemset2DAsync");
+    return hip_check(kiln::launch_zero_rows(out, (size_t)ldo * esz, (size_t)H * Dh * esz, Tq, s), "zero_rows launch");
 }
 
 int flash_self(void* out, DT od, int ldo, long long bso, const void* q, int ldq, long long bsq, const void* k, int ldk,
@@ -143,7 +165,9 @@ int flash_self(void* out, DT od, int ldo, long long bso, const void* q, int ldq,
     return hip_check(kiln::launch_attn_fwd(a, stream), "attn_fwd launch");
 }
 
-}  // namespace
+}  // namespace kiln::capi
+
+using namespace kiln::capi;
 
 extern "C" {
 
@@ -159,6 +183,73 @@ const char* kiln_attn_status_string(int status) {
 }
 
 const char* kiln_attn_last_error(void) { return g_err; }
+
+size_t kiln_attn_dropin_workspace_bytes(int Tq, int Tk, int H) {
+    if (Tq <= 0 || Tk <= 0 || H <= 0) return 0;
+    const int ks = kiln::attn_key_split(1, Tq, Tk, H);
+    return kiln_kv_prepped_bytes(Tk, H) + kiln::attn_split_bytes(ks, 1, Tq, H);
+}
+
+int kiln_attn_workspace_reserve(size_t bytes) {
+    int dev = 0;
+    if (int r = current_device(&dev)) return r;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace& w = ws_of(dev);
+    if (w.fixed && !w.owned) return fail(KILN_EINVAL, "device %d has a caller-bound workspace", dev);
+    if (w.bytes < bytes) {
+        // set-up time: earlier users of the library's buffers finish before they are released
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_check(e, "hipDeviceSynchronize");
+        drop_owned(w);
+        void* p = nullptr;
+        e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return fail(KILN_ENOMEM, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        w.ptr = p;
+        w.bytes = bytes;
+        w.owned = true;
+    }
+    w.fixed = true;
+    return KILN_OK;
+}
+
+int kiln_attn_set_workspace(void* ptr, size_t bytes) {
+    int dev = 0;
+    if (int r = current_device(&dev)) return r;
+    if (ptr && ((uintptr_t)ptr & 255)) return fail(KILN_EUNSUPPORTED, "workspace must be 256-byte aligned");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace& w = ws_of(dev);
+    if (w.owned) {
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_check(e, "hipDeviceSynchronize");
+        drop_owned(w);
+    }
+    std::vector<void*> old;
+    old.swap(w.old);
+    w = Workspace{};
+    w.old.swap(old);
+    if (ptr) {
+        w.ptr = ptr;
+        w.bytes = bytes;
+        w.fixed = true;
+    }
+    return KILN_OK;
+}
+
+int kiln_attn_workspace_release(void) {
+    int dev = 0;
+    if (int r = current_device(&dev)) return r;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace& w = ws_of(dev);
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_check(e, "hipDeviceSynchronize");
+    if (w.owned || !w.ptr) {
+        drop_owned(w);
+    } else {  // a caller-bound buffer stays bound; only outgrown library buffers go
+        for (void* p : w.old) (void)hipFree(p);
+        w.old.clear();
+    }
+    return KILN_OK;
+}
 
 int kiln_attn_device_arch(int dev, char* buf, int buflen) {
     hipDeviceProp_t prop;
@@ -729,6 +820,14 @@ int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next
     if (!(sigma > 0.f)) return fail(KILN_EINVAL, "flow_euler_step: sigma %g must be > 0", (double)sigma);
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_flow_euler(x, v, sigma, sigma_next, n, (hipStream_t)stream), "flow_euler launch");
+}
+
+int kiln_flow_euler_den(float* x, const float* den, float sigma, float sigma_next, size_t n, kiln_stream_t stream) {
+    if (n && (!x || !den)) return fail(KILN_EINVAL, "flow_euler_den: null pointer");
+    if (!(sigma > 0.f)) return fail(KILN_EINVAL, "flow_euler_den: sigma %g must be > 0", (double)sigma);
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_flow_euler_den(x, den, sigma, sigma_next, n, (hipStream_t)stream),
+                     "flow_euler_den launch");
 }
 
 int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {

@@ -186,6 +186,15 @@ __global__ void k_flow_euler(float* __restrict__ x, const float* __restrict__ v,
     }
 }
 
+// k_euler_step on a given denoised estimate (the masked path): the same expression as k_flow_euler
+__global__ void k_flow_euler_den(float* __restrict__ x, const float* __restrict__ den, float s, float sn, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float xi = x[i];
+        x[i] = xi + (xi - den[i]) / s * (sn - s);
+    }
+}
+
 // first-block step cache (engine/src/dit.cu:327-340): y = a - b, and the relative L1 change sum|a - b| / sum|b|
 // as two sums (acc[0], acc[1]) that the host divides
 __global__ void k_sub(float* __restrict__ y, const float* __restrict__ a, const float* __restrict__ b, size_t n) {
@@ -314,6 +323,11 @@ hipError_t launch_flow_start(float* x, const float* noise, const float* init, fl
 }
 hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(k_flow_euler, dim3(nblk(n)), dim3(256), 0, st, x, v, s, sn, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_flow_euler_den(float* x, const float* den, float s, float sn, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_flow_euler_den, dim3(nblk(n)), dim3(256), 0, st, x, den, s, sn, n);
     return hipGetLastError();
 }
 

@@ -2,6 +2,7 @@
 // and the exact fp32 attention used when the fp16 path does not apply (causal, Dh != 128, fp32 mode).
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -376,6 +377,24 @@ hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const
     if (Tq <= 0 || H <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_exact_attn, dim3(Tq, H), dim3(256), 0, s, out, ldo, q, ldq, k, ldk, v, ldv, Tk, Dh,
                        causal ? 1 : 0, npad, 1.f / sqrtf((float)Dh));
+    return hipGetLastError();
+}
+
+// rows x cols 16-bit units of a strided matrix set to zero (the output of a call with only padding keys). A
+// kernel rather than hipMemset2DAsync, so a call can be captured into a HIP graph.
+__global__ void k_zero_rows(uint16_t* out, size_t ld, size_t cols, int rows) {
+    const size_t n = cols * (size_t)rows;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[(i / cols) * ld + i % cols] = 0;
+}
+
+hipError_t launch_zero_rows(void* out, size_t ld_bytes, size_t row_bytes, int rows, hipStream_t s) {
+    if (rows <= 0 || row_bytes == 0) return hipSuccess;
+    if (ld_bytes % 2 || row_bytes % 2 || (uintptr_t)out % 2) return hipErrorInvalidValue;
+    const size_t n = row_bytes / 2 * (size_t)rows;
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_zero_rows, dim3(blocks), dim3(256), 0, s, static_cast<uint16_t*>(out), ld_bytes / 2,
+                       row_bytes / 2, rows);
     return hipGetLastError();
 }
 

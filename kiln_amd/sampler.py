@@ -10,21 +10,31 @@ import math
 
 import numpy as np
 
-from . import (cfg_combine, flow_denoised, flow_denoised_masked, flow_ersde_step, flow_euler_step, flow_inpaint_in,
-               flow_start, flow_update, torch_randn)
+from . import (cfg_combine, flow_denoised, flow_denoised_masked, flow_ersde_step, flow_euler_den, flow_euler_step,
+               flow_inpaint_in, flow_start, flow_update, torch_randn)
 
 
 def flow_sigmas(steps, shift=1.0, denoise=1.0):
     """The "simple" schedule over ModelSamplingDiscreteFlow (engine/src/pipeline.cu:66-78): 1000 shifted sigmas
     t' = shift t / (1 + (shift - 1) t), t = (i + 1) / 1000, sampled every 1000 / total entries from the top,
     then 0; the last steps + 1 values (total = steps / denoise for partial denoising)."""
-    total = steps if denoise > 0.9999 else int(steps / denoise)
+    total = steps if not _denoise_partial(denoise) else _denoise_total(steps, denoise)
     t = (np.arange(1000, dtype=np.float32) + np.float32(1)) / np.float32(1000)
     shift = np.float32(shift)
     table = t if shift == 1 else (shift * t / (np.float32(1) + (shift - np.float32(1)) * t)).astype(np.float32)
     ss = 1000.0 / total
     s = [float(table[999 - int(x * ss)]) for x in range(total)] + [0.0]
     return s[len(s) - (steps + 1):]
+
+
+def _denoise_partial(denoise):
+    """denoise > 0.9999f in the reference's float32 (pipeline.cu:67, 266): False means the full schedule."""
+    return not (np.float32(denoise) > np.float32(0.9999))
+
+
+def _denoise_total(steps, denoise):
+    """(int)((double)steps / (double)denoise) with the reference's float32 denoise (pipeline.cu:67, 268)."""
+    return int(float(steps) / float(np.float32(denoise)))
 
 
 SAMPLERS = ("euler", "euler_ancestral", "dpmpp_2m", "res_multistep", "er_sde")
@@ -107,11 +117,11 @@ def _full_schedule(name, steps, shift):
 
 def schedule_sigmas(name, steps, shift=1.0, denoise=1.0):
     """schedule_sigmas (engine/src/pipeline.cu:265-277): the schedule of steps / denoise steps, last steps + 1."""
-    if denoise > 0.9999:
+    if not _denoise_partial(denoise):
         return _full_schedule(name, steps, shift)
-    if denoise <= 0:
+    if np.float32(denoise) <= 0:
         return []
-    s = _full_schedule(name, int(steps / denoise), shift)
+    s = _full_schedule(name, _denoise_total(steps, denoise), shift)
     return s if len(s) < steps + 1 else s[len(s) - (steps + 1):]
 
 
@@ -205,11 +215,9 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
     if mask is not None and init is None:
         raise ValueError("an inpainting mask needs init")
     xin = torch.empty_like(x) if mask is not None else x
+    sigmas = list(sigmas)
     if sampler == "er_sde":
         oldd = torch.empty_like(x)
-        sigmas = list(sigmas)
-        if sigmas[0] >= 1.0:
-            sigmas[0] = 1.0 - 1e-4  # lambda = sigma / (1 - sigma) needs sigma < 1 (pipeline.cu:482)
     cfg_steps = math.ceil(cfg_until * steps - 1e-4) if negative else 0
     warm = max(2, math.ceil(cache_start * steps))
     tail = max(1, math.ceil((1.0 - cache_end) * steps))
@@ -218,6 +226,10 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
     if cache is not None:
         cache.skips = 0
     flow_start(x, noise, sigmas[0], init)
+    if sampler == "er_sde" and np.float32(sigmas[0]) >= 1:
+        # lambda = sigma / (1 - sigma) needs sigma < 1; the start above used the unclamped sigma
+        # (pipeline.cu:481-482), the clamp is float32 1 - 1e-4f
+        sigmas[0] = float(np.float32(1) - np.float32(1e-4))
     for i in range(steps):
         s = sigmas[i]
         cfg_now = i < cfg_steps
@@ -240,7 +252,7 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
         if sampler == "euler" and mask is None:
             flow_euler_step(x, v, s, sn)
         elif sampler == "euler":
-            flow_update(x, den, sn / s, 1.0 - sn / s)
+            flow_euler_den(x, den, s, sn)
         elif sampler == "er_sde":
             if mask is None:
                 flow_denoised(den, x, v, s)
@@ -270,4 +282,8 @@ def sample_euler(model, x, noise, sigmas, cfg=1.0, cfg_until=1.0, timestep_mult=
         if sampler != "euler" or mask is not None:
             den, old = old, den
             have_old = True
+    last = float(np.float32(sigmas[-1]))
+    if 0.0 < last < 1.0:
+        # stopped above sigma 0 (leftover noise for a second pass): x / (1 - sigma) (pipeline.cu:583-588)
+        flow_update(x, x, float(np.float32(1) / (np.float32(1) - np.float32(last))), 0.0)
     return x

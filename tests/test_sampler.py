@@ -238,3 +238,93 @@ def test_ersde_sampling_runs_deterministically(gpu):
         sampler.sample_euler(model, x, n, sig, negative=False, sampler="er_sde", seed=9)
         runs.append(x.cpu())
     assert torch.isfinite(runs[0]).all() and torch.equal(runs[0], runs[1])
+
+
+def test_partial_denoise_uses_float32_denoise():
+    """The reference computes total = (int)((double)steps / (double)denoise) with denoise a float
+    (engine/src/pipeline.cu:67, 268): float32(0.8) = 0.800000011920929 makes 4 / 0.8 fall just below 5, so the
+    schedule has 4 steps and steps 4 at denoise 0.8 is the full schedule from sigma 1."""
+    np.testing.assert_allclose(sampler.flow_sigmas(4, 1.0, 0.8), [1.0, 0.75, 0.5, 0.25, 0.0], rtol=0, atol=1e-7)
+    np.testing.assert_allclose(sampler.flow_sigmas(3, 1.0, 0.6), [0.75, 0.5, 0.25, 0.0], rtol=0, atol=1e-7)
+    np.testing.assert_allclose(sampler.flow_sigmas(1, 1.0, 0.2), [0.25, 0.0], rtol=0, atol=1e-7)
+    np.testing.assert_allclose(sampler.schedule_sigmas("simple", 4, 1.0, 0.8), [1.0, 0.75, 0.5, 0.25, 0.0],
+                               rtol=0, atol=1e-7)
+    # the full-schedule test is float32 too: 0.99995 rounds above 0.9999f
+    assert sampler.flow_sigmas(4, 1.0, 0.99995) == sampler.flow_sigmas(4, 1.0)
+
+
+@pytest.mark.gpu
+def test_euler_stopping_above_zero_hands_back_leftover_noise(gpu):
+    """A schedule that stops at sigma_last in (0, 1) returns x / (1 - sigma_last) (engine/src/pipeline.cu:583-588).
+    On a straight trajectory x(s) = s n + (1 - s) x0 Euler is exact, so the result is x0 + s / (1 - s) n."""
+    g = torch.Generator().manual_seed(15)
+    x0, n = torch.randn(16, 4, 6, generator=g), torch.randn(16, 4, 6, generator=g)
+    vd = (n - x0).to(DEV)
+
+    def model(outs, xx, t, cfg_now):
+        outs[0].copy_(vd)
+
+    sig = sampler.flow_sigmas(6, 3.0)[:4]
+    s = sig[-1]
+    assert 0 < s < 1
+    x = torch.empty(16, 4, 6, device=DEV)
+    sampler.sample_euler(model, x, n.to(DEV), sig, negative=False)
+    np.testing.assert_allclose(x.cpu().numpy(), (x0 + s / (1 - s) * n).numpy(), rtol=0, atol=5e-5)
+
+
+@pytest.mark.gpu
+def test_masked_euler_is_bit_identical_with_a_full_mask(gpu):
+    """With mask 1 everywhere the masked Euler path computes the reference's k_euler_step expression on the same
+    denoised values as the unmasked path (engine/src/pipeline.cu:326-331), so the results are bit-identical."""
+    g = torch.Generator().manual_seed(16)
+    init, n = torch.randn(16, 4, 6, generator=g).to(DEV), torch.randn(16, 4, 6, generator=g).to(DEV)
+
+    def model(outs, xx, t, cfg_now):
+        outs[0].copy_(0.7 * xx - 0.3 * init)
+
+    sig = sampler.flow_sigmas(5, 3.0, 0.8)
+    ref, x1 = torch.empty_like(init), torch.empty_like(init)
+    sampler.sample_euler(model, ref, n, sig, negative=False, init=init)
+    sampler.sample_euler(model, x1, n, sig, negative=False, init=init, mask=torch.ones(4, 6, device=DEV))
+    assert torch.equal(x1, ref)
+
+
+@pytest.mark.gpu
+def test_ersde_trajectory_against_float64(gpu):
+    """The er_sde loop (engine/src/pipeline.cu:481-482, 538-547) on a constant-velocity model against a float64
+    statement of it: x starts at sigma_0 = 1 exactly (x = noise), then sigma_0 is clamped to float32(1 - 1e-4f)
+    for the coefficients; stages 1-3 use the previous denoised values and first differences; the last step
+    goes to the denoised estimate; noise torch_randn(seed + 1 + i)."""
+    g = torch.Generator().manual_seed(17)
+    x0, n = torch.randn(16, 4, 6, generator=g), torch.randn(16, 4, 6, generator=g)
+    vd = (n - x0).to(DEV)
+
+    def model(outs, xx, t, cfg_now):
+        outs[0].copy_(vd)
+
+    sig = sampler.flow_sigmas(6, 3.0)
+    assert sig[0] == 1.0
+    x = torch.empty(16, 4, 6, device=DEV)
+    sampler.sample_euler(model, x, n.to(DEV), sig, negative=False, sampler="er_sde", seed=9)
+
+    sc = list(sig)
+    sc[0] = float(np.float32(1) - np.float32(1e-4))
+    xr, v = n.double().clone(), (n - x0).double()
+    old = oldd = None
+    for i in range(6):
+        den = xr - v * sc[i]
+        if sc[i + 1] == 0.0:
+            xr = den
+            break
+        a, b, c2, inv2, c3, inv3, cn, stage = sampler.ersde_coef(sc, i)
+        nz = kiln_amd.torch_randn(9 + 1 + i, xr.numel()).view_as(xr).double()
+        xn = a * xr + b * den
+        if stage >= 2:
+            d1 = (den - old) * inv2
+            xn = xn + c2 * d1
+            if stage >= 3:
+                xn = xn + c3 * (d1 - oldd) * inv3
+            oldd = d1
+        xr = xn + cn * nz
+        old = den
+    np.testing.assert_allclose(x.cpu().double().numpy(), xr.numpy(), rtol=0, atol=1e-4)

@@ -82,6 +82,18 @@ int kiln_attn_fwd_f32out(float* out, int ldo, const float* q, int ldq, const flo
 int kiln_attn_fwd_f16out(uint16_t* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                          int ldv, int Tq, int Tk, int H, int Dh, int npad, kiln_stream_t stream);
 
+/* attention16 (kiln_attn_fwd_f16out, same arguments, results and errors) for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. No
+ * counterpart in the reference. Its scratch (fp16 K/V tiles, key-split partials) is a fixed device array of
+ * kiln_attn_noalloc_scratch_bytes() (64 MiB) per device, held until the process ends; a call whose K/V tiles
+ * (kiln_kv_prepped_bytes(Tk, H)) exceed it returns KILN_ENOMEM. It calls no hipMalloc/hipFree and never
+ * synchronizes. Every call on one device shares that device's scratch: calls that overlap on one GPU (e.g. on
+ * two streams) race. */
+int kiln_attn_fwd_f16out_noalloc(uint16_t* out, int ldo, const float* q, int ldq, const float* k, int ldk,
+                                 const float* v, int ldv, int Tq, int Tk, int H, int Dh, int npad,
+                                 kiln_stream_t stream);
+size_t kiln_attn_noalloc_scratch_bytes(void);
+
 /* Exact fp32 attention (the reference's fallback when G.fp16 is off: --fp32 / "precision":"fp32",
  * engine/src/kernels.cu:840-865): any Dh <= 256, optional causal mask, npad. */
 int kiln_attn_fwd_exact(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,

@@ -62,6 +62,8 @@ _SIGS = {
     "kiln_attn_workspace_reserve": (_i, [_sz]),
     "kiln_attn_set_workspace": (_i, [_vp, _sz]),
     "kiln_attn_workspace_release": (_i, []),
+    "kiln_attn_fwd_f16out_noalloc": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "kiln_attn_noalloc_scratch_bytes": (_sz, []),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "kiln_linear16_prepped_weight_bytes": (_sz, [_i, _i]),
     "kiln_linear16_prepare_weight": (_i, [_vp, _vp, _i, _i, _i, _vp]),

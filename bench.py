@@ -146,61 +146,53 @@ def dit_step_case(torch, kiln_amd, dev, nblocks=28, Hp=48, Wp=72, B=2, L=512, se
 
 
 def dit_forward_case(torch, kiln_amd, dev, nblocks=28, ndistinct=4, Hp=48, Wp=72, B=2, L=512, seed=200):
-    """One DiT forward of the CFG pair at config 5 on the fp16-activation path (kiln_amd.dit.forward16, the
-    reference's Dit::forward_batch, engine/src/dit.cu:357-546, without the step cache): step tables (timestep
-    MLP + the 28 blocks' adaLN matvecs), patch embedding, 28 blocks (modulated LayerNorms, the Q/K/V, O,
-    cross-Q, cross-O and MLP linear16 GEMMs with fused epilogues, fused self-attention, cross-attention +
-    NAG), final layer and unpatchify. 2B shapes (D = 2048, 16 heads, MLP 8192), random-init weights prepared
-    at load; 4 distinct blocks cycled (472 MB of weights, more than the 256 MB MALL, as 28 distinct blocks
-    would be); contexts (positive, unconditional, NAG negative, L = 512) prepared per block outside the step."""
+    """One DiT forward of the CFG pair at config 5 on the fp16-activation path through the C++ step driver
+    (kiln_amd.dit.Dit -> libkiln_dit.so, the reference's Dit::forward_batch, engine/src/dit.cu:357-546, without
+    the step cache): step tables (timestep MLP + the 28 blocks' adaLN matvecs), patch embedding, 28 blocks
+    (modulated LayerNorms, the Q/K/V, O, cross-Q, cross-O and MLP linear16 GEMMs with fused epilogues, fused
+    self-attention, cross-attention + NAG), final layer and unpatchify. 2B shapes (D = 2048, 16 heads, MLP 8192),
+    random-init bf16 weights (torch Linear's default init; 4 distinct weight sets, each block holding its own
+    copy prepared at load); contexts (positive, unconditional, NAG negative, L = 512) cached outside the step.
+    Also an 8-step Euler sampling run (kiln_dit_sample: the whole loop in C++)."""
     from kiln_amd import dit
     T, Dm = Hp * Wp, H * D
     g = torch.Generator(device=dev).manual_seed(seed)
-    c, s = kiln_amd.cosmos_rope_tables(Hp, Wp)
-    rope = (c.to(dev), s.to(dev))
     nw = torch.ones(D, dtype=torch.bfloat16, device=dev)
 
     def bf(o, i):
         return linear_init(torch, o, i, g, dev).to(torch.bfloat16)
 
-    distinct, ctx = [], [[], [], []]
+    d = dit.Dit(nblocks, H, ctx_dim=1024)
+    sets = []
     for _ in range(ndistinct):
-        w = [linear_init(torch, o, i, g, dev).half() for o, i in
-             [(3 * Dm, Dm), (Dm, Dm), (Dm, Dm), (Dm, Dm), (4 * Dm, Dm), (Dm, 4 * Dm)]]
-        ck, cv = linear_init(torch, Dm, 1024, g, dev), linear_init(torch, Dm, 1024, g, dev)
-        blk = dit.Block16(*w, nw, nw, nw, nw, ca_k=ck, ca_v=cv,
-                          mod=[bf(256, Dm), bf(3 * Dm, 256), bf(256, Dm), bf(3 * Dm, 256), bf(256, Dm), bf(3 * Dm, 256)])
-        del w
-        for j in range(3):
-            ctx[j].append(blk.prepare_context(torch.randn(L, 1024, generator=g, device=dev)))
-        distinct.append(blk)
-    blocks = [distinct[i % ndistinct] for i in range(nblocks)]
-    kv = [[ctx[j][i % ndistinct] for i in range(nblocks)] for j in range(3)]
-    sw = dit.StepWeights(bf(Dm, Dm), bf(3 * Dm, Dm), torch.ones(Dm, dtype=torch.bfloat16, device=dev), bf(256, Dm),
-                         bf(2 * Dm, 256), bf(Dm, 68), bf(64, Dm))
-    ws = dit.Workspace(B, T, Dm, 4 * Dm, dev)
+        sets.append(dict(sa_q=bf(Dm, Dm), sa_k=bf(Dm, Dm), sa_v=bf(Dm, Dm), sa_o=bf(Dm, Dm), ca_q=bf(Dm, Dm),
+                         ca_o=bf(Dm, Dm), ca_k=bf(Dm, 1024), ca_v=bf(Dm, 1024), mlp1=bf(4 * Dm, Dm),
+                         mlp2=bf(Dm, 4 * Dm), sa_qn=nw, sa_kn=nw, ca_qn=nw, ca_kn=nw,
+                         mod=[bf(256, Dm), bf(3 * Dm, 256), bf(256, Dm), bf(3 * Dm, 256), bf(256, Dm),
+                              bf(3 * Dm, 256)]))
+    for i in range(nblocks):
+        d.set_block(i, **sets[i % ndistinct])
+    del sets
+    d.set_step_weights(bf(Dm, Dm), bf(3 * Dm, Dm), torch.ones(Dm, dtype=torch.bfloat16, device=dev), bf(256, Dm),
+                       bf(2 * Dm, 256), bf(Dm, 68), bf(64, Dm))
+    cs = [d.cache_context(torch.randn(L, 1024, generator=g, device=dev)) for _ in range(3)]
     latent = torch.randn(16, 2 * Hp, 2 * Wp, generator=g, device=dev)
     outs = [torch.empty_like(latent) for _ in range(B)]
+    nag = dit.Nag(cs[2], 5.0, 2.5, 0.25)
 
     def step():
-        dit.forward16(outs, latent, 0.5, sw, blocks, ws, B, rope, [(kv[0], L, 0), (kv[1], L, 0)],
-                      nag=(kv[2], L, 0, 5.0, 2.5, 0.25))
+        d.forward(outs, latent, 0.5, cs[:2], nag=nag)
 
-    from kiln_amd import sampler
     noise = torch.randn_like(latent)
     x = torch.empty_like(latent)
 
-    def model(o, xx, t, cfg_now):  # the CFG pair in one batched forward (NAG on the prompt item)
-        dit.forward16(o, xx, t, sw, blocks, ws, B, rope, [(kv[0], L, 0), (kv[1], L, 0)],
-                      nag=(kv[2], L, 0, 5.0, 2.5, 0.25))
-
-    def sample8():  # 8 Euler steps, shift 3, CFG 4.5 on every step, timestep = sigma (multiplier 1)
-        sampler.sample_euler(model, x, noise, sampler.flow_sigmas(8, 3.0), cfg=4.5)
+    def sample8():  # 8 Euler steps, shift 3, CFG 4.5 on every step (the pair batched), NAG on the prompt item
+        d.sample(x, cs[0], neg=cs[1], nag=nag, steps=8, shift=3.0, cfg=4.5, noise=noise)
 
     R = B * T
     gemm = 2.0 * R * Dm * Dm * 6 + 2 * 2.0 * R * 4 * Dm * Dm
     attn = 4.0 * B * H * T * T * D + 4.0 * (B + 1) * H * T * L * D
-    return dict(step=step, sample8=sample8, flop=nblocks * (gemm + attn))
+    return dict(step=step, sample8=sample8, flop=nblocks * (gemm + attn), dit=d, contexts=cs)
 
 
 def linear16_cases(torch, kiln_amd, tm, dev, steps, warmup):

@@ -192,6 +192,10 @@ int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* 
                     kiln_stream_t stream);
 /* First-block step cache (engine/src/dit.cu:327-340, used at :404-433): y = a - b (k_sub), and the two sums of
  * the relative L1 change, acc[0] = sum |a - b|, acc[1] = sum |b| (device float[2], overwritten; k_rel_l1). */
+/* Odd latent sides (engine/src/dit.cu:342-370): circular padding of a latent [16, Hs, Ws] to [16, Hd, Wd]
+ * (k_pad_circular), and the crop of [16, Hs, Ws] to its top-left [16, Hd, Wd] (k_crop). */
+int kiln_pad_circular(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln_stream_t stream);
+int kiln_crop(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln_stream_t stream);
 int kiln_sub(float* y, const float* a, const float* b, size_t n, kiln_stream_t stream);
 int kiln_rel_l1(const float* a, const float* b, size_t n, float* acc, kiln_stream_t stream);
 /* Replaces torch_randn() (engine/src/pipeline.cu:17-64): host memory out[n] = torch.manual_seed(seed);

@@ -14,6 +14,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkiln_attn.so")
+HOST = os.path.join(HERE, "host")
+DIT_LIB = os.path.join(HERE, "libkiln_dit.so")
+DIT_SOURCES = ["dit.cpp", "sampler.cpp", "capi_dit.cpp"]
 SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -25,10 +28,10 @@ FLAGS = [
 ]
 
 
-def _compile(src):
+def _compile(src, where=CSRC):
     out = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
     lang = ["-x", "hip"]
-    cmd = [HIPCC, *lang, *FLAGS, "-c", os.path.join(CSRC, src), "-o", out]
+    cmd = [HIPCC, *lang, *FLAGS, "-c", os.path.join(where, src), "-o", out]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -48,6 +51,18 @@ def build(verbose=False):
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)
+    # the step driver (host C++ over the C ABI above), linked against libkiln_attn.so
+    with ThreadPoolExecutor(max_workers=len(DIT_SOURCES)) as ex:
+        dobjs = list(ex.map(lambda f: _compile(f, HOST), DIT_SOURCES))
+    tmp = DIT_LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *dobjs, "-L" + HERE, "-lkiln_attn",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, DIT_LIB)
+    if verbose:
+        print("built", DIT_LIB)
     return LIB
 
 

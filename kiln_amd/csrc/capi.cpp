@@ -746,6 +746,18 @@ int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream
     return hip_check(kiln::launch_cfg_combine(v, vn, cfg, n, (hipStream_t)stream), "cfg_combine launch");
 }
 
+int kiln_pad_circular(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln_stream_t stream) {
+    if (Hs <= 0 || Ws <= 0 || Hd <= 0 || Wd <= 0) return fail(KILN_EINVAL, "pad_circular: bad sizes");
+    if (!dst || !src) return fail(KILN_EINVAL, "pad_circular: null pointer");
+    return hip_check(kiln::launch_pad_circular(dst, src, Hs, Ws, Hd, Wd, (hipStream_t)stream), "pad_circular launch");
+}
+
+int kiln_crop(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln_stream_t stream) {
+    if (Hs <= 0 || Ws <= 0 || Hd <= 0 || Wd <= 0 || Hd > Hs || Wd > Ws) return fail(KILN_EINVAL, "crop: bad sizes");
+    if (!dst || !src) return fail(KILN_EINVAL, "crop: null pointer");
+    return hip_check(kiln::launch_crop(dst, src, Hs, Ws, Hd, Wd, (hipStream_t)stream), "crop launch");
+}
+
 int kiln_sub(float* y, const float* a, const float* b, size_t n, kiln_stream_t stream) {
     if (n && (!y || !a || !b)) return fail(KILN_EINVAL, "sub: null pointer");
     if (!n) return KILN_OK;

@@ -195,6 +195,25 @@ __global__ void k_flow_euler_den(float* __restrict__ x, const float* __restrict_
     }
 }
 
+// latents [16, H, W] with an odd side go through the forward on the 2x2 patch grid: circular padding to
+// [16, Hd, Wd] and a crop back (engine/src/dit.cu:342-370)
+__global__ void k_pad_circular(float* __restrict__ dst, const float* __restrict__ src, int Hs, int Ws, int Hd, int Wd) {
+    const size_t n = (size_t)16 * Hd * Wd;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int x = (int)(i % Wd), y = (int)((i / Wd) % Hd);
+    const size_t c = i / ((size_t)Wd * Hd);
+    dst[i] = src[(c * Hs + y % Hs) * Ws + x % Ws];
+}
+__global__ void k_crop(float* __restrict__ dst, const float* __restrict__ src, int Hs, int Ws, int Hd, int Wd) {
+    const size_t n = (size_t)16 * Hd * Wd;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int x = (int)(i % Wd), y = (int)((i / Wd) % Hd);
+    const size_t c = i / ((size_t)Wd * Hd);
+    dst[i] = src[(c * Hs + y) * Ws + x];
+}
+
 // first-block step cache (engine/src/dit.cu:327-340): y = a - b, and the relative L1 change sum|a - b| / sum|b|
 // as two sums (acc[0], acc[1]) that the host divides
 __global__ void k_sub(float* __restrict__ y, const float* __restrict__ a, const float* __restrict__ b, size_t n) {
@@ -328,6 +347,17 @@ hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t
 
 hipError_t launch_flow_euler_den(float* x, const float* den, float s, float sn, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(k_flow_euler_den, dim3(nblk(n)), dim3(256), 0, st, x, den, s, sn, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_pad_circular(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, hipStream_t st) {
+    const size_t n = (size_t)16 * Hd * Wd;
+    hipLaunchKernelGGL(k_pad_circular, dim3(nblk(n)), dim3(256), 0, st, dst, src, Hs, Ws, Hd, Wd);
+    return hipGetLastError();
+}
+hipError_t launch_crop(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, hipStream_t st) {
+    const size_t n = (size_t)16 * Hd * Wd;
+    hipLaunchKernelGGL(k_crop, dim3(nblk(n)), dim3(256), 0, st, dst, src, Hs, Ws, Hd, Wd);
     return hipGetLastError();
 }
 

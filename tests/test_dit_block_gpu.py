@@ -1,5 +1,6 @@
-"""One DiT block on the fp16-activation path (kiln_amd.dit.block_forward16, composed of the library's entry
-points) against a float64 restatement of the reference's block loop (engine/src/dit.cu:458-493).
+"""The DiT through the C++ step driver (libkiln_dit.so, kiln_amd.dit.Dit): one block on the fp16-activation path
+against a float64 restatement of the reference's block loop (engine/src/dit.cu:458-493), the whole forward, the
+step cache and the fp32 block; plus the DiT's auxiliary kernels.
 
 The restatement rounds to fp16 where the reference's fp16 path stores fp16 (the modulated LayerNorm output,
 the attention outputs, the NAG combine, the GELU output) and keeps everything else exact, so the difference
@@ -62,123 +63,162 @@ REALS = [40, 64, 33]  # prompt, unconditional, NAG negative: real rows of 64-row
 NAG = (5.0, 2.5, 0.25)
 
 
-def _make_block(g):
-    def w16(o, i):
-        return (torch.randn(o, i, generator=g) * i ** -0.5).half()
+def _bf16w(g, o, i, scale=None):
+    return _bf16(torch.randn(o, i, generator=g) * (scale if scale is not None else i ** -0.5))
 
-    w = dict(qkv=w16(3 * D, D), o=w16(D, D), cq=w16(D, D), co=w16(D, D), w1=w16(F, D), w2=w16(D, F),
-             ck=torch.randn(D, DCTX, generator=g) * DCTX ** -0.5, cv=torch.randn(D, DCTX, generator=g) * DCTX ** -0.5,
-             nw=[_bf16(1 + 0.2 * torch.randn(HD, generator=g)) for _ in range(4)])
-    blk = dit.Block16(w["qkv"].to(DEV), w["o"].to(DEV), w["cq"].to(DEV), w["co"].to(DEV), w["w1"].to(DEV),
-                      w["w2"].to(DEV), *[v.to(DEV) for v in w["nw"]], ca_k=w["ck"].to(DEV), ca_v=w["cv"].to(DEV))
-    return w, blk
+
+def _block_weights(g):
+    """Random bf16 weights of one block [out, in] (host), as a checkpoint holds them."""
+    w = dict(sa_q=_bf16w(g, D, D), sa_k=_bf16w(g, D, D), sa_v=_bf16w(g, D, D), sa_o=_bf16w(g, D, D),
+             ca_q=_bf16w(g, D, D), ca_o=_bf16w(g, D, D), ca_k=_bf16w(g, D, DCTX), ca_v=_bf16w(g, D, DCTX),
+             mlp1=_bf16w(g, F, D), mlp2=_bf16w(g, D, F))
+    for n in ("sa_qn", "sa_kn", "ca_qn", "ca_kn"):
+        w[n] = _bf16(1 + 0.2 * torch.randn(HD, generator=g))
+    w["mod"] = [_bf16w(g, 256, D), _bf16w(g, 3 * D, 256), _bf16w(g, 256, D), _bf16w(g, 3 * D, 256),
+                _bf16w(g, 256, D), _bf16w(g, 3 * D, 256)]
+    return w
+
+
+def _make_dit(g, nblocks):
+    """A Dit of nblocks random blocks (H = 4, D = 512, F = 2048, 256-wide contexts) and random step weights."""
+    d = dit.Dit(nblocks, H, ctx_dim=DCTX, mlp=F, eps=EPS)
+    ws = []
+    for i in range(nblocks):
+        w = _block_weights(g)
+        d.set_block(i, **{k: (v.to(DEV) if torch.is_tensor(v) else [m.to(DEV) for m in v]) for k, v in w.items()})
+        ws.append(w)
+    sw = dict(t_lin1=_bf16w(g, D, D), t_lin2=_bf16w(g, 3 * D, D), t_norm=_bf16(1 + 0.1 * torch.randn(D, generator=g)),
+              final_mod1=_bf16w(g, 256, D), final_mod2=_bf16w(g, 2 * D, 256), x_embed=_bf16w(g, D, 68, 68 ** -0.5),
+              final_lin=_bf16w(g, 64, D))
+    d.set_step_weights(**{k: v.to(DEV) for k, v in sw.items()})
+    return d, ws, sw
+
+
+def _h(w):
+    """A linear16 weight as the fp16 path uses it: bf16 converted to fp16 at load (weight_to_f16)."""
+    return w.float().half().double()
+
+
+def _ctx_kv(w, c):
+    """Dit::cache_context (engine/src/dit.cu:217-234): K = rmsnorm(ctx W_k^T; ca_kn), V = ctx W_v^T."""
+    k = _rms(c.double() @ w["ca_k"].float().double().T, w["ca_kn"].float().double(), H, EPS)
+    return k, c.double() @ w["ca_v"].float().double().T
 
 
 def _ref_block(x, mods, w, ctxs, rc, rs):
     """float64 restatement of one block (engine/src/dit.cu:458-493), fp16 rounding where the fp16 path stores."""
     d = lambda t: t.double()  # noqa: E731
-    nw = [d(v.float()) for v in w["nw"]]
+    nw = {k: d(w[k].float()) for k in ("sa_qn", "sa_kn", "ca_qn")}
     mo, mc, mm = d(mods[:3 * D]), d(mods[3 * D:6 * D]), d(mods[6 * D:])
     n = _ln16(x, mo[:D], mo[D:2 * D], EPS)
-    qkv = n @ d(w["qkv"]).T
     a = torch.empty(B * T, D, dtype=torch.float64)
     for b in range(B):
         rows = slice(b * T, (b + 1) * T)
-        q = _rope(_rms(qkv[rows, :D], nw[0], H, EPS), d(rc), d(rs), H)
-        k = _rope(_rms(qkv[rows, D:2 * D], nw[1], H, EPS), d(rc), d(rs), H)
-        a[rows] = _r16(_attn(q, k, qkv[rows, 2 * D:], H))
-    x = x + mo[2 * D:] * (a @ d(w["o"]).T)
+        q = _rope(_rms(n[rows] @ _h(w["sa_q"]).T, nw["sa_qn"], H, EPS), d(rc), d(rs), H)
+        k = _rope(_rms(n[rows] @ _h(w["sa_k"]).T, nw["sa_kn"], H, EPS), d(rc), d(rs), H)
+        a[rows] = _r16(_attn(q, k, n[rows] @ _h(w["sa_v"]).T, H))
+    x = x + mo[2 * D:] * (a @ _h(w["sa_o"]).T)
     n = _ln16(x, mc[:D], mc[D:2 * D], EPS)
-    qc = _rms(n @ d(w["cq"]).T, nw[2], H, EPS)
-    kc = [_rms(d(c) @ d(w["ck"]).T, nw[3], H, EPS) for c in ctxs]
-    vc = [d(c) @ d(w["cv"]).T for c in ctxs]
+    qc = _rms(n @ _h(w["ca_q"]).T, nw["ca_qn"], H, EPS)
+    kv = [_ctx_kv(w, c) for c in ctxs]
     for b in range(B):
         rows = slice(b * T, (b + 1) * T)
-        a[rows] = _r16(_attn(qc[rows], kc[b], vc[b], H, L - REALS[b]))
-    an = _r16(_attn(qc[:T], kc[2], vc[2], H, L - REALS[2]))
+        a[rows] = _r16(_attn(qc[rows], kv[b][0], kv[b][1], H, L - REALS[b]))
+    an = _r16(_attn(qc[:T], kv[2][0], kv[2][1], H, L - REALS[2]))
     a[:T] = _r16(torch.from_numpy(oracle.nag(a[:T].numpy(), an.numpy(), *NAG)).double())
-    x = x + mc[2 * D:] * (a @ d(w["co"]).T)
+    x = x + mc[2 * D:] * (a @ _h(w["ca_o"]).T)
     n = _ln16(x, mm[:D], mm[D:2 * D], EPS)
-    h = n @ d(w["w1"]).T
+    h = n @ _h(w["mlp1"]).T
     h = _r16(0.5 * h * (1 + torch.erf(h / np.sqrt(2))))
-    return x + mm[2 * D:] * (h @ d(w["w2"]).T)
+    return x + mm[2 * D:] * (h @ _h(w["mlp2"]).T)
 
 
 def test_dit_block_forward16_matches_reference(gpu):
+    """One block (Dit::run_block, fp16 path) with random modulation and contexts cached by the driver."""
     g = torch.Generator().manual_seed(31)
-    w, blk = _make_block(g)
+    d, ws, _ = _make_dit(g, 1)
     mods = torch.randn(9 * D, generator=g) * 0.3
     X0 = torch.randn(B * T, D, generator=g)
     ctxs = [torch.randn(r, DCTX, generator=g) for r in REALS]
-    kvs = [blk.prepare_context(c.to(DEV), EPS) for c in ctxs]
+    cc = [d.cache_context(c.to(DEV), length=L) for c in ctxs]
     rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
-    ws = dit.Workspace(B, T, D, F, DEV)
     X = X0.to(DEV).clone()
-    dit.block_forward16(X, mods.to(DEV), blk, ws, B, T, (rc.to(DEV), rs.to(DEV)),
-                        [(kvs[i], REALS[i], L - REALS[i]) for i in range(B)],
-                        nag=(kvs[2], REALS[2], L - REALS[2]) + NAG, eps=EPS)
+    d.run_block(0, X, mods.to(DEV), Hp, Wp, cc[:B], nag=dit.Nag(cc[2], *NAG))
     torch.cuda.synchronize()
-    x = _ref_block(X0.double(), mods, w, ctxs, rc, rs)
+    x = _ref_block(X0.double(), mods, ws[0], ctxs, rc, rs)
     err = (X.cpu().double() - x).abs()
     assert torch.isfinite(X).all()
     assert err.max().item() <= 1e-2 and err.mean().item() <= 5e-4, (err.max().item(), err.mean().item())
 
 
-def _bf16w(g, o, i, scale=None):
-    return _bf16(torch.randn(o, i, generator=g) * (scale if scale is not None else i ** -0.5))
+def _sinusoid(t):
+    """The timestep sinusoid of Dit::step_tables (engine/src/dit.cu:246-251) in float32: cos(t e_i), sin(t e_i),
+    e_i = exp(-i ln(10000) / (D/2))."""
+    i = np.arange(D // 2, dtype=np.float32)
+    e = np.exp(i * np.float32(-np.log(np.float32(10000.0))) / np.float32(D // 2)).astype(np.float32)
+    te = (np.float32(t) * e).astype(np.float32)
+    return np.concatenate([np.cos(te), np.sin(te)]).astype(np.float32)
 
 
-def test_dit_forward16_two_blocks_matches_reference(gpu):
-    """Dit::forward_batch on the fp16 path (engine/src/dit.cu:357-546) with two blocks: step tables (timestep
-    sinusoid, t_embedder MLP, adaLN modulation matvecs), patch embedding, the blocks, the final modulated
-    LayerNorm + linear and unpatchify, against a float64 restatement. Bar on the output latents (~N(0,1)):
-    max-abs 2e-2, mean-abs 1e-3."""
-    g = torch.Generator().manual_seed(32)
-    Hl, Wl, t = 2 * Hp, 2 * Wp, 0.73
-    blocks, ws_ = [], []
-    for _ in range(2):
-        w, blk = _make_block(g)
-        mod = [_bf16w(g, 256, D), _bf16w(g, 3 * D, 256), _bf16w(g, 256, D), _bf16w(g, 3 * D, 256),
-               _bf16w(g, 256, D), _bf16w(g, 3 * D, 256)]
-        blk.mod = [m.to(DEV) for m in mod]
-        w["mod"] = mod
-        blocks.append(blk)
-        ws_.append(w)
-    sw_h = dict(t_lin1=_bf16w(g, D, D), t_lin2=_bf16w(g, 3 * D, D), t_norm=_bf16(1 + 0.1 * torch.randn(D, generator=g)),
-                f1=_bf16w(g, 256, D), f2=_bf16w(g, 2 * D, 256), xe=_bf16w(g, D, 68, 68 ** -0.5), fl=_bf16w(g, 64, D))
-    sw = dit.StepWeights(*[sw_h[k].to(DEV) for k in ("t_lin1", "t_lin2", "t_norm", "f1", "f2", "xe", "fl")])
-    ctxs = [torch.randn(r, DCTX, generator=g) for r in REALS]
-    kv = [[blk.prepare_context(c.to(DEV), EPS) for blk in blocks] for c in ctxs]
-    latent = torch.randn(16, Hl, Wl, generator=g)
-    rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
-    ws = dit.Workspace(B, T, D, F, DEV)
-    outs = [torch.empty(16, Hl, Wl, device=DEV) for _ in range(B)]
-    dit.forward16(outs, latent.to(DEV), t, sw, blocks, ws, B, (rc.to(DEV), rs.to(DEV)),
-                  [(kv[i], REALS[i], L - REALS[i]) for i in range(B)], nag=(kv[2], REALS[2], L - REALS[2]) + NAG,
-                  eps=EPS)
-    torch.cuda.synchronize()
-
+def _ref_forward(t, ws, sw, latent, ctxs, rc, rs, Hl, Wl):
     d = lambda a: a.double() if torch.is_tensor(a) else torch.from_numpy(a).double()  # noqa: E731
     bw = lambda a: d(a.float())  # noqa: E731
     silu = lambda v: v / (1 + torch.exp(-v))  # noqa: E731
-    s = d(dit.timestep_sinusoid(t, D))
-    lora = bw(sw_h["t_lin2"]) @ silu(bw(sw_h["t_lin1"]) @ s)
-    temb = silu(s / torch.sqrt((s * s).mean() + EPS) * bw(sw_h["t_norm"]))
+    s = d(_sinusoid(t))
+    lora = bw(sw["t_lin2"]) @ silu(bw(sw["t_lin1"]) @ s)
+    temb = silu(s / torch.sqrt((s * s).mean() + EPS) * bw(sw["t_norm"]))
     tok = d(oracle.patchify(latent.numpy()))
-    x = (tok @ bw(sw_h["xe"]).T).repeat(B, 1)
-    for blk_w in ws_:
-        mods = torch.cat([bw(blk_w["mod"][2 * j + 1]) @ (bw(blk_w["mod"][2 * j]) @ temb) + lora for j in range(3)])
-        x = _ref_block(x, mods.float(), blk_w, ctxs, rc, rs)
-    fmod = bw(sw_h["f2"]) @ (bw(sw_h["f1"]) @ temb) + lora[:2 * D]
+    x = (tok @ bw(sw["x_embed"]).T).repeat(B, 1)
+    for w in ws:
+        mods = torch.cat([bw(w["mod"][2 * j + 1]) @ (bw(w["mod"][2 * j]) @ temb) + lora for j in range(3)])
+        x = _ref_block(x, mods.float(), w, ctxs, rc, rs)
+    fmod = bw(sw["final_mod2"]) @ (bw(sw["final_mod1"]) @ temb) + lora[:2 * D]
     m = x.mean(-1, keepdim=True)
     var = ((x - m) ** 2).mean(-1, keepdim=True)
     n = (x - m) / torch.sqrt(var + EPS) * (1 + fmod[D:]) + fmod[:D]
-    y = n @ bw(sw_h["fl"]).T
+    y = n @ bw(sw["final_lin"]).T
+    return [oracle.unpatchify(y[b * T:(b + 1) * T].float().numpy(), Hl, Wl).astype(np.float64) for b in range(B)]
+
+
+def test_dit_forward16_two_blocks_matches_reference(gpu):
+    """Dit::forward_batch on the fp16 path (engine/src/dit.cu:357-546) with two blocks, through the C++ driver:
+    step tables (timestep sinusoid, t_embedder MLP, adaLN modulation matvecs), patch embedding, the blocks, the
+    final modulated LayerNorm + linear and unpatchify, against a float64 restatement. Bar on the output latents
+    (~N(0,1)): max-abs 2e-2, mean-abs 1e-3."""
+    g = torch.Generator().manual_seed(32)
+    Hl, Wl, t = 2 * Hp, 2 * Wp, 0.73
+    d, ws, sw = _make_dit(g, 2)
+    ctxs = [torch.randn(r, DCTX, generator=g) for r in REALS]
+    cc = [d.cache_context(c.to(DEV), length=L) for c in ctxs]
+    latent = torch.randn(16, Hl, Wl, generator=g)
+    rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
+    outs = [torch.empty(16, Hl, Wl, device=DEV) for _ in range(B)]
+    d.forward(outs, latent.to(DEV), t, cc[:B], nag=dit.Nag(cc[2], *NAG))
+    torch.cuda.synchronize()
+    refs = _ref_forward(t, ws, sw, latent, ctxs, rc, rs, Hl, Wl)
     for b in range(B):
-        ref = oracle.unpatchify(y[b * T:(b + 1) * T].float().numpy(), Hl, Wl).astype(np.float64)
-        err = np.abs(outs[b].cpu().double().numpy() - ref)
+        err = np.abs(outs[b].cpu().double().numpy() - refs[b])
         assert np.isfinite(err).all()
         assert err.max() <= 2e-2 and err.mean() <= 1e-3, (b, err.max(), err.mean())
+
+
+def test_dit_forward_odd_latent_pads_circularly(gpu):
+    """An odd latent side runs on the circularly padded 2x2 patch grid and is cropped back (engine/src/dit.cu:
+    359-371): the result equals the top-left crop of the forward of the padded latent."""
+    g = torch.Generator().manual_seed(37)
+    d, _, _ = _make_dit(g, 1)
+    cc = [d.cache_context(torch.randn(r, DCTX, generator=g).to(DEV), length=L) for r in REALS[:B]]
+    Hl, Wl = 2 * Hp - 1, 2 * Wp - 1
+    lat = torch.randn(16, Hl, Wl, generator=g).to(DEV)
+    padded = torch.cat([lat, lat[:, :1]], 1)
+    padded = torch.cat([padded, padded[:, :, :1]], 2).contiguous()
+    o_odd = [torch.empty(16, Hl, Wl, device=DEV) for _ in range(B)]
+    o_pad = [torch.empty(16, Hl + 1, Wl + 1, device=DEV) for _ in range(B)]
+    d.forward(o_odd, lat, 0.5, cc)
+    d.forward(o_pad, padded, 0.5, cc)
+    torch.cuda.synchronize()
+    for a, b_ in zip(o_odd, o_pad):
+        assert torch.equal(a, b_[:, :Hl, :Wl].contiguous())
 
 
 @pytest.mark.parametrize("rows,cols", [(256, 2048), (6144, 256), (37, 100)])
@@ -240,37 +280,26 @@ def test_matvec_bf16_grouped(gpu):
 
 
 def test_step_cache_skip_reuses_residual(gpu):
-    """First-block step cache (engine/src/dit.cu:404-433, 532-536): a second forward whose block-0 residual did
-    not move skips blocks 1..N-1 and returns the same latents (block-0 output + the cached residual); with
-    allow off it runs in full; the relative-L1 and difference kernels against numpy."""
+    """First-block step cache (engine/src/dit.cu:404-433, 532-536) in the C++ driver: a second forward whose
+    block-0 residual did not move skips blocks 1..N-1 and returns the same latents (block-0 output + the cached
+    residual); with allow off it runs in full; the relative-L1 and difference kernels against numpy."""
     g = torch.Generator().manual_seed(33)
-    blocks = []
-    for _ in range(3):
-        _, blk = _make_block(g)
-        blk.mod = [_bf16w(g, 256, D).to(DEV), _bf16w(g, 3 * D, 256).to(DEV)] * 3
-        blocks.append(blk)
-    sw = dit.StepWeights(_bf16w(g, D, D).to(DEV), _bf16w(g, 3 * D, D).to(DEV), _bf16(torch.ones(D)).to(DEV),
-                         _bf16w(g, 256, D).to(DEV), _bf16w(g, 2 * D, 256).to(DEV), _bf16w(g, D, 68).to(DEV),
-                         _bf16w(g, 64, D).to(DEV))
-    ctxs = [torch.randn(r, DCTX, generator=g).to(DEV) for r in REALS]
-    kv = [[blk.prepare_context(c, EPS) for blk in blocks] for c in ctxs]
-    rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
-    ws = dit.Workspace(B, T, D, F, DEV)
+    d, _, _ = _make_dit(g, 3)
+    cc = [d.cache_context(torch.randn(r, DCTX, generator=g).to(DEV), length=L) for r in REALS[:B]]
     latent = torch.randn(16, 2 * Hp, 2 * Wp, generator=g).to(DEV)
-    args = (0.4, sw, blocks, ws, B, (rc.to(DEV), rs.to(DEV)), [(kv[i], REALS[i], L - REALS[i]) for i in range(B)])
     sc = dit.StepCache(0.05)
     sc.allow = True
     o1 = [torch.empty_like(latent) for _ in range(B)]
-    dit.forward16(o1, latent, *args, sc=sc)
+    d.forward(o1, latent, 0.4, cc, cache=sc)
     assert not sc.skipped and sc.valid
     o2 = [torch.empty_like(latent) for _ in range(B)]
-    dit.forward16(o2, latent, *args, sc=sc)
+    d.forward(o2, latent, 0.4, cc, cache=sc)
     assert sc.skipped and sc.last_change == 0.0
     for a, b in zip(o1, o2):
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
     sc.allow = False
     o3 = [torch.empty_like(latent) for _ in range(B)]
-    dit.forward16(o3, latent, *args, sc=sc)
+    d.forward(o3, latent, 0.4, cc, cache=sc)
     assert not sc.skipped
     for a, b in zip(o1, o3):
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
@@ -349,22 +378,18 @@ def test_dit_cross_attn_x16_fused_projection(gpu):
 
 def test_dit_block_forward32_matches_reference(gpu):
     """The fp32 branch of the block (engine/src/dit.cu:495-530: fp32 linears with bf16 weights, exact fp32
-    attention, fp32 GELU) against the float64 restatement without fp16 roundings: max-abs 1e-3, mean-abs 5e-5."""
+    attention, fp32 GELU), Dit::run_block(fp32=True), against the float64 restatement without fp16 roundings:
+    max-abs 1e-3, mean-abs 5e-5."""
     g = torch.Generator().manual_seed(36)
-    bw = lambda o, i: _bf16w(g, o, i)  # noqa: E731
-    Wq, Wk, Wv, Wo, Wcq, Wco, W1, W2 = bw(D, D), bw(D, D), bw(D, D), bw(D, D), bw(D, D), bw(D, D), bw(F, D), bw(D, F)
-    nw = [_bf16(1 + 0.2 * torch.randn(HD, generator=g)) for _ in range(4)]
-    blk = dit.Block32(*[w.to(DEV) for w in (Wq, Wk, Wv, Wo, Wcq, Wco, W1, W2)], nw[0].to(DEV), nw[1].to(DEV),
-                      nw[2].to(DEV))
+    d_, ws, _ = _make_dit(g, 1)
+    w = ws[0]
     mods = torch.randn(9 * D, generator=g) * 0.3
     X0 = torch.randn(B * T, D, generator=g)
-    ctx = [(_rms(torch.randn(r, D, generator=g).double(), nw[3].float().double(), H, EPS).float(),
-            torch.randn(r, D, generator=g)) for r in REALS]
+    ctxs = [torch.randn(r, DCTX, generator=g) for r in REALS]
+    cc = [d_.cache_context(c.to(DEV), length=L, fp32=True) for c in ctxs]
     rc, rs = kiln_amd.cosmos_rope_tables(Hp, Wp)
     X = X0.to(DEV).clone()
-    dit.block_forward32(X, mods.to(DEV), blk, B, T, (rc.to(DEV), rs.to(DEV)),
-                        [(ctx[i][0].to(DEV), ctx[i][1].to(DEV), L - REALS[i]) for i in range(B)],
-                        nag=(ctx[2][0].to(DEV), ctx[2][1].to(DEV), L - REALS[2]) + NAG, eps=EPS)
+    d_.run_block(0, X, mods.to(DEV), Hp, Wp, cc[:B], nag=dit.Nag(cc[2], *NAG), fp32=True)
     torch.cuda.synchronize()
     d = lambda t: t.double()  # noqa: E731
     bf = lambda t: t.float().double()  # noqa: E731
@@ -376,24 +401,63 @@ def test_dit_block_forward32_matches_reference(gpu):
         return (x - m) / torch.sqrt(((x - m) ** 2).mean(-1, keepdim=True) + EPS) * (1 + sc) + sh
 
     n = ln(x, mo[:D], mo[D:2 * D])
-    q, k, v = n @ bf(Wq).T, n @ bf(Wk).T, n @ bf(Wv).T
+    q, k, v = n @ bf(w["sa_q"]).T, n @ bf(w["sa_k"]).T, n @ bf(w["sa_v"]).T
     a = torch.empty(B * T, D, dtype=torch.float64)
     for b in range(B):
         r_ = slice(b * T, (b + 1) * T)
-        a[r_] = _attn(_rope(_rms(q[r_], bf(nw[0]), H, EPS), d(rc), d(rs), H),
-                      _rope(_rms(k[r_], bf(nw[1]), H, EPS), d(rc), d(rs), H), v[r_], H)
-    x = x + mo[2 * D:] * (a @ bf(Wo).T)
+        a[r_] = _attn(_rope(_rms(q[r_], bf(w["sa_qn"]), H, EPS), d(rc), d(rs), H),
+                      _rope(_rms(k[r_], bf(w["sa_kn"]), H, EPS), d(rc), d(rs), H), v[r_], H)
+    x = x + mo[2 * D:] * (a @ bf(w["sa_o"]).T)
     n = ln(x, mc[:D], mc[D:2 * D])
-    qc = _rms(n @ bf(Wcq).T, bf(nw[2]), H, EPS)
+    qc = _rms(n @ bf(w["ca_q"]).T, bf(w["ca_qn"]), H, EPS)
+    kv = [_ctx_kv(w, c) for c in ctxs]
     for b in range(B):
         r_ = slice(b * T, (b + 1) * T)
-        a[r_] = _attn(qc[r_], d(ctx[b][0]), d(ctx[b][1]), H, L - REALS[b])
-    an = _attn(qc[:T], d(ctx[2][0]), d(ctx[2][1]), H, L - REALS[2])
+        a[r_] = _attn(qc[r_], kv[b][0], kv[b][1], H, L - REALS[b])
+    an = _attn(qc[:T], kv[2][0], kv[2][1], H, L - REALS[2])
     a[:T] = torch.from_numpy(oracle.nag(a[:T].numpy(), an.numpy(), *NAG)).double()
-    x = x + mc[2 * D:] * (a @ bf(Wco).T)
+    x = x + mc[2 * D:] * (a @ bf(w["ca_o"]).T)
     n = ln(x, mm[:D], mm[D:2 * D])
-    h = n @ bf(W1).T
+    h = n @ bf(w["mlp1"]).T
     h = 0.5 * h * (1 + torch.erf(h / np.sqrt(2)))
-    x = x + mm[2 * D:] * (h @ bf(W2).T)
+    x = x + mm[2 * D:] * (h @ bf(w["mlp2"]).T)
     err = (X.cpu().double() - x).abs()
     assert err.max().item() <= 1e-3 and err.mean().item() <= 5e-5, (err.max().item(), err.mean().item())
+
+
+def test_dit_sample_in_cpp_matches_the_python_driven_loop(gpu):
+    """kiln_dit_sample (sample() with the DiT as its model, the whole loop in C++: pipeline.cu:415-598) against
+    the same sampler driving Dit.forward from Python: CFG of the pair in one batched forward with NAG on the
+    prompt is bit-identical; the unbatched CFG path (prompt pass with NAG, negative pass without) agrees to
+    fp16-path noise; NAG switched off below nag_sigma_end changes the result."""
+    from kiln_amd import sampler
+    g = torch.Generator().manual_seed(38)
+    d, _, _ = _make_dit(g, 2)
+    cc = [d.cache_context(torch.randn(r, DCTX, generator=g).to(DEV), length=L) for r in REALS]
+    nag = dit.Nag(cc[2], *NAG)
+    shape = (16, 2 * Hp, 2 * Wp)
+    noise = torch.randn(*shape, generator=g).to(DEV)
+    kw = dict(steps=4, shift=3.0, cfg=3.0, cfg_until=0.5, seed=7, noise=noise)
+
+    def model(outs, x, t, cfg_now):
+        if cfg_now:
+            d.forward(outs, x, t, cc[:2], nag=nag)
+        else:
+            d.forward(outs[:1], x, t, cc[:1], nag=nag)
+
+    ref = torch.empty(*shape, device=DEV)
+    sampler.sample_euler(model, ref, noise, sampler.flow_sigmas(4, 3.0), cfg=3.0, cfg_until=0.5)
+    x = torch.empty_like(ref)
+    d.sample(x, cc[0], neg=cc[1], nag=nag, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(x).all() and torch.equal(x, ref)
+    xu = torch.empty_like(ref)
+    d.sample(xu, cc[0], neg=cc[1], nag=nag, batch_cfg=False, **kw)
+    torch.cuda.synchronize()
+    assert (xu - ref).abs().max().item() <= 2e-2
+    xo = torch.empty_like(ref)
+    d.sample(xo, cc[0], neg=cc[1], nag=nag, nag_sigma_end=2.0, **kw)  # every sigma < 2: NAG never applies
+    xn = torch.empty_like(ref)
+    d.sample(xn, cc[0], neg=cc[1], **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(xo, xn) and not torch.equal(xo, x)

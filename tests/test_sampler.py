@@ -57,7 +57,8 @@ def test_flow_kernels_and_euler_cfg_loop(gpu):
         if i < 2:
             vp = 0.25 * xr + 4.0 * (vp - 0.25 * xr)
         xr = xr + vp * (sig[i + 1] - sig[i])
-    assert calls == [(round(s * 1000.0, 6), i < 2) for i, s in enumerate(sig[:-1])]
+    # the model's timestep is float32 sigma * timestep_mult (pipeline.cu:484)
+    assert calls == [(round(float(np.float32(s) * np.float32(1000.0)), 6), i < 2) for i, s in enumerate(sig[:-1])]
     np.testing.assert_allclose(xg.cpu().numpy(), xr, rtol=1e-4, atol=1e-4)
 
 
@@ -66,7 +67,9 @@ def test_step_cache_guards(gpu):
     """The sampler's cache guards (engine/src/pipeline.cu:463-480): no skip before max(2, ceil(0.15 steps)), none
     in the last max(1, ceil(0.1 steps)) steps, at most cache_max_hits in a row. A stub model records `allow` and
     skips whenever allowed."""
-    from kiln_amd import dit
+    class Cache:  # a stand-in with the attributes the sampler reads and sets
+        def __init__(self, threshold):
+            self.threshold, self.allow, self.skipped, self.skips = threshold, False, False, 0
 
     class Stub:
         def __init__(self, cache):
@@ -77,7 +80,7 @@ def test_step_cache_guards(gpu):
             self.cache.skipped = self.cache.allow
             outs[0].zero_()
 
-    sc = dit.StepCache(0.1)
+    sc = Cache(0.1)
     stub = Stub(sc)
     x = torch.empty(16, 4, 4, device=DEV)
     sampler.sample_euler(stub, x, torch.zeros(16, 4, 4, device=DEV), sampler.flow_sigmas(20, 3.0), negative=False,
@@ -91,12 +94,13 @@ def test_step_cache_guards(gpu):
 @pytest.mark.parametrize("name", ["euler", "dpmpp_2m", "res_multistep"])
 def test_step_coef_exact_on_linear_trajectories(name):
     """Every step x <- a x + b den + c old (engine/src/pipeline.cu:396-411) must keep a point of a straight flow
-    trajectory x(s) = x0 + s (n - x0) on it when den = old = x0: a = s'/s and b + c = 1 - s'/s."""
+    trajectory x(s) = x0 + s (n - x0) on it when den = old = x0: a = s'/s and b + c = 1 - s'/s (to float32, the
+    coefficients' type in the reference)."""
     sig = sampler.flow_sigmas(10, 3.0)
     for i in range(10):
         a, b, c = sampler.step_coef(name, sig, i, i > 0)
         sn, s = sig[i + 1], sig[i]
-        assert abs(a - sn / s) < 1e-12 and abs(b + c - (1 - sn / s)) < 1e-12
+        assert abs(a - sn / s) < 1e-6 and abs(b + c - (1 - sn / s)) < 1e-6
     # first step and the step to sigma 0 are first order
     assert sampler.step_coef(name, sig, 0, False)[2] == 0.0 and sampler.step_coef(name, sig, 9, True)[2] == 0.0
 
@@ -196,7 +200,7 @@ def test_ersde_coefficients_keep_the_data_point():
     sig[0] = 1.0 - 1e-4
     for i in range(7):
         a, b, c2, inv2, c3, inv3, cn, stage = sampler.ersde_coef(sig, i)
-        assert abs(a * (1 - sig[i]) + b - (1 - sig[i + 1])) < 1e-9
+        assert abs(a * (1 - sig[i]) + b - (1 - sig[i + 1])) < 1e-6  # float32 coefficients, as the reference
         assert cn >= 0 and stage == min(3, i + 1)
 
 

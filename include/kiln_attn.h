@@ -192,6 +192,9 @@ int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* 
                     kiln_stream_t stream);
 /* First-block step cache (engine/src/dit.cu:327-340, used at :404-433): y = a - b (k_sub), and the two sums of
  * the relative L1 change, acc[0] = sum |a - b|, acc[1] = sum |b| (device float[2], overwritten; k_rel_l1). */
+/* Synthetic weights (no reference counterpart: the reference loads checkpoints): p[i] = bf16 of lo + (hi - lo) u_i,
+ * u_i uniform in [0, 1) from a counter-based hash of (seed, i); lo == hi fills a constant. */
+int kiln_fill_uniform_bf16(uint16_t* p, size_t n, uint64_t seed, float lo, float hi, kiln_stream_t stream);
 /* Odd latent sides (engine/src/dit.cu:342-370): circular padding of a latent [16, Hs, Ws] to [16, Hd, Wd]
  * (k_pad_circular), and the crop of [16, Hs, Ws] to its top-left [16, Hd, Wd] (k_crop). */
 int kiln_pad_circular(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln_stream_t stream);

@@ -59,6 +59,7 @@ _SIGS = {
     "kiln_flow_euler_step": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
     "kiln_flow_euler_den": (_i, [_vp, _vp, _f, _f, _sz, _vp]),
     "kiln_pad_circular": (_i, [_vp, _vp, _i, _i, _i, _i, _vp]),
+    "kiln_fill_uniform_bf16": (_i, [_vp, _sz, ctypes.c_uint64, _f, _f, _vp]),
     "kiln_crop": (_i, [_vp, _vp, _i, _i, _i, _i, _vp]),
     "kiln_attn_dropin_workspace_bytes": (_sz, [_i, _i, _i]),
     "kiln_attn_workspace_reserve": (_i, [_sz]),

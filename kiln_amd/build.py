@@ -17,6 +17,7 @@ LIB = os.path.join(HERE, "libkiln_attn.so")
 HOST = os.path.join(HERE, "host")
 DIT_LIB = os.path.join(HERE, "libkiln_dit.so")
 DIT_SOURCES = ["dit.cpp", "sampler.cpp", "capi_dit.cpp"]
+ENGINE = os.path.join(HERE, "kiln_engine")
 SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -63,6 +64,17 @@ def build(verbose=False):
     os.replace(tmp, DIT_LIB)
     if verbose:
         print("built", DIT_LIB)
+    # the engine process (JSON-lines protocol) over the driver
+    eobj = _compile("engine_main.cpp", HOST)
+    tmp = ENGINE + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", eobj, "-L" + HERE, "-lkiln_dit", "-lkiln_attn", "-lpthread",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, ENGINE)
+    if verbose:
+        print("built", ENGINE)
     return LIB
 
 

@@ -758,6 +758,13 @@ int kiln_crop(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln
     return hip_check(kiln::launch_crop(dst, src, Hs, Ws, Hd, Wd, (hipStream_t)stream), "crop launch");
 }
 
+int kiln_fill_uniform_bf16(uint16_t* p, size_t n, uint64_t seed, float lo, float hi, kiln_stream_t stream) {
+    if (n && !p) return fail(KILN_EINVAL, "fill_uniform_bf16: null pointer");
+    if (!(lo <= hi)) return fail(KILN_EINVAL, "fill_uniform_bf16: lo > hi");
+    if (!n) return KILN_OK;
+    return hip_check(kiln::launch_fill_uniform_bf16(p, n, seed, lo, hi, (hipStream_t)stream), "fill_uniform launch");
+}
+
 int kiln_sub(float* y, const float* a, const float* b, size_t n, kiln_stream_t stream) {
     if (n && (!y || !a || !b)) return fail(KILN_EINVAL, "sub: null pointer");
     if (!n) return KILN_OK;

@@ -9,6 +9,8 @@
 //   unpatchify   latent [16, Hl, Wl] from tok [T, 64]                                dit.cu:184-191
 //   linear_f32   y [T, rows] = x [T, cols] W^T, W bf16 [rows, cols], fp32 MFMA      kernels.cu:508-529 (linear)
 //   cfg_combine  v = vn + cfg (v - vn)                                              kernels.cu:1058-1062
+#include <algorithm>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -214,6 +216,24 @@ __global__ void k_crop(float* __restrict__ dst, const float* __restrict__ src, i
     dst[i] = src[(c * Hs + y) * Ws + x];
 }
 
+// Synthetic weights: p[i] = bf16(lo + (hi - lo) u_i), u_i in [0, 1) from a counter-based hash of (seed, i)
+// (SplitMix64's finalizer, a published 64-bit mixer), so a weight set is a pure function of its seed.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+__global__ void k_fill_uniform_bf16(uint16_t* __restrict__ p, size_t n, uint64_t seed, float lo, float hi) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const uint64_t h = mix64(seed * 0x9e3779b97f4a7c15ULL + i + 1);
+        const float u = (float)(h >> 40) * (1.0f / 16777216.0f);
+        const float v = lo + (hi - lo) * u;
+        uint32_t bits = __float_as_uint(v);
+        bits += 0x7FFF + ((bits >> 16) & 1);  // round to nearest even
+        p[i] = (uint16_t)(bits >> 16);
+    }
+}
+
 // first-block step cache (engine/src/dit.cu:327-340): y = a - b, and the relative L1 change sum|a - b| / sum|b|
 // as two sums (acc[0], acc[1]) that the host divides
 __global__ void k_sub(float* __restrict__ y, const float* __restrict__ a, const float* __restrict__ b, size_t n) {
@@ -358,6 +378,12 @@ hipError_t launch_pad_circular(float* dst, const float* src, int Hs, int Ws, int
 hipError_t launch_crop(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, hipStream_t st) {
     const size_t n = (size_t)16 * Hd * Wd;
     hipLaunchKernelGGL(k_crop, dim3(nblk(n)), dim3(256), 0, st, dst, src, Hs, Ws, Hd, Wd);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_uniform_bf16(uint16_t* p, size_t n, uint64_t seed, float lo, float hi, hipStream_t st) {
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(k_fill_uniform_bf16, dim3(blocks), dim3(256), 0, st, p, n, seed, lo, hi);
     return hipGetLastError();
 }
 

@@ -115,6 +115,7 @@ hipError_t launch_flow_update(float* x, const float* den, const float* old, floa
 hipError_t launch_flow_euler(float* x, const float* v, float s, float sn, size_t n, hipStream_t st);
 hipError_t launch_pad_circular(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, hipStream_t st);
 hipError_t launch_crop(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, hipStream_t st);
+hipError_t launch_fill_uniform_bf16(uint16_t* p, size_t n, uint64_t seed, float lo, float hi, hipStream_t st);
 hipError_t launch_zero_rows(void* out, size_t ld_bytes, size_t row_bytes, int rows, hipStream_t s);
 hipError_t launch_flow_euler_den(float* x, const float* den, float s, float sn, size_t n, hipStream_t st);
 

@@ -93,3 +93,17 @@ def test_argument_checks_return_before_any_gpu_call():
     sig = (ctypes.c_float * 2)(1.0, 0.0)
     assert L.kiln_step_coef(b"euler", sig, 2, 1, 0, abc) == kiln_amd.KILN_EINVAL  # i + 1 beyond the schedule
     assert L.kiln_step_coef(b"euler", sig, 2, 0, 0, abc) == 0 and abs(abc[0]) < 1e-12 and abs(abc[1] - 1) < 1e-7
+
+
+def test_engine_reports_fatal_without_a_device():
+    """kiln_engine's start-up failure path (main.cpp:647-660: a fatal event, exit code 1), on a machine without
+    a GPU; the protocol itself is tested on the GPU (tests/test_engine_protocol_gpu.py)."""
+    import subprocess
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "kiln_amd", "kiln_engine")
+    r = subprocess.run([exe], input='{"cmd":"info","id":"x"}\n', capture_output=True, text=True, timeout=60)
+    import json
+    ev = [json.loads(ln) for ln in r.stdout.splitlines() if ln.strip()]
+    assert r.returncode == 1 and ev and ev[-1]["ev"] == "fatal" and ev[-1]["msg"]

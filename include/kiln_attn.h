@@ -66,6 +66,20 @@ int kiln_attn_set_workspace(void* ptr, size_t bytes);
 int kiln_attn_workspace_release(void);
 
 /* ------------------------------------------------------------------------------------------
+ * Per-category GPU timing (replaces the reference's ProfScope / prof_enable / prof_report,
+ * engine/src/kernels.cu:14-58, gpu.h:92-99). While enabled, every entry point records a hipEvent pair
+ * on its stream under its category: attention (all attention entry points and the K/V prepare),
+ * gemm_tc16 (linear16 and the projections of the fused DiT sections), gemm_fp32, matvec, norm,
+ * layernorm, rope, nag, eltwise, w->f16. Not for use under HIP graph capture.
+ * ------------------------------------------------------------------------------------------ */
+/* on != 0 starts a new profile (clears the previous one); 0 stops recording. */
+int kiln_prof_enable(int on);
+/* Waits for the recorded events and writes one line per category ("name ms percent (calls)") and a sum line. */
+int kiln_prof_report(char* buf, size_t buflen);
+/* The summed milliseconds and call count of one category. */
+int kiln_prof_category(const char* name, double* ms, int* calls);
+
+/* ------------------------------------------------------------------------------------------
  * Drop-in replacements of the reference op layer
  * ------------------------------------------------------------------------------------------ */
 

@@ -65,6 +65,9 @@ _SIGS = {
     "kiln_attn_workspace_reserve": (_i, [_sz]),
     "kiln_attn_set_workspace": (_i, [_vp, _sz]),
     "kiln_attn_workspace_release": (_i, []),
+    "kiln_prof_enable": (_i, [_i]),
+    "kiln_prof_report": (_i, [ctypes.c_char_p, _sz]),
+    "kiln_prof_category": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i)]),
     "kiln_attn_fwd_f16out_noalloc": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "kiln_attn_noalloc_scratch_bytes": (_sz, []),
     "kiln_linear16_prepped": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
@@ -113,6 +116,26 @@ def lib():
             fn.argtypes = args
         _LIB = L
     return _LIB
+
+
+def prof_enable(on=True):
+    """Starts (or stops) per-category GPU timing of the library's entry points (the reference's --profile)."""
+    _check(lib().kiln_prof_enable(int(bool(on))))
+
+
+def prof_report():
+    """The per-category report of the current profile: {category: (ms, calls)} and its text form."""
+    buf = ctypes.create_string_buffer(1 << 14)
+    _check(lib().kiln_prof_report(buf, len(buf)))
+    text = buf.value.decode()
+    cats = {}
+    for ln in text.splitlines():
+        parts = ln.split()
+        if len(parts) >= 3 and parts[0] != "sum":
+            ms, calls = ctypes.c_double(), ctypes.c_int()
+            _check(lib().kiln_prof_category(parts[0].encode(), ctypes.byref(ms), ctypes.byref(calls)))
+            cats[parts[0]] = (ms.value, calls.value)
+    return cats, text
 
 
 def header_symbols(path=HEADER_PATH):

@@ -267,6 +267,7 @@ size_t kiln_kv_prepped_bytes(int Tk, int H) {
 int kiln_kv_prepare(uint16_t* kvp, const void* k, int ldk, const void* v, int ldv, int in_dtype, int Tk, int H,
                     const uint16_t* k_norm_w, float eps, const float* rope_cos, const float* rope_sin,
                     kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     if (in_dtype != KILN_F32 && in_dtype != KILN_F16) return fail(KILN_EINVAL, "in_dtype %d", in_dtype);
     DT in = (DT)in_dtype;
     if (Tk < 0 || H <= 0) return fail(KILN_EINVAL, "bad sizes Tk=%d H=%d", Tk, H);
@@ -285,6 +286,7 @@ int kiln_kv_prepare(uint16_t* kvp, const void* k, int ldk, const void* v, int ld
 int kiln_attn_fwd_prepped(void* out, int out_dtype, int ldo, const void* q, int in_dtype, int ldq,
                           const uint16_t* q_norm_w, float eps, const float* rope_cos, const float* rope_sin,
                           const uint16_t* kvp, int Tq, int Tk, int H, int npad, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
         return fail(KILN_EINVAL, "dtype");
     int r = check_common(Tq, Tk, H, npad);
@@ -316,6 +318,7 @@ int kiln_attn_fwd_prepped_batch(void* out, int out_dtype, int ldo, long long bso
                                 long long bsq, const uint16_t* q_norm_w, float eps, const float* rope_cos,
                                 const float* rope_sin, const uint16_t* const* kvp, int B, int Tq, int Tk, int H,
                                 int npad, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
         return fail(KILN_EINVAL, "dtype");
     int r = check_common(Tq, Tk, H, npad);
@@ -349,6 +352,7 @@ int kiln_attn_fwd_prepped_batch(void* out, int out_dtype, int ldo, long long bso
 
 int kiln_attn_fwd_f32out(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                          int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     int r = check_common(Tq, Tk, H, npad);
     if (r) return r;
     if (Tq == 0) return KILN_OK;
@@ -363,6 +367,7 @@ int kiln_attn_fwd_f32out(float* out, int ldo, const float* q, int ldq, const flo
 
 int kiln_attn_fwd_f16out(uint16_t* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                          int ldv, int Tq, int Tk, int H, int Dh, int npad, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     int r = check_common(Tq, Tk, H, npad);
     if (r) return r;
     if (Dh != 128) return fail(KILN_EUNSUPPORTED, "attention16: unsupported head size %d (needs 128)", Dh);
@@ -377,6 +382,7 @@ int kiln_attn_fwd_f16out(uint16_t* out, int ldo, const float* q, int ldq, const 
 
 int kiln_attn_fwd_exact(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                         int ldv, int Tq, int Tk, int H, int Dh, int causal, int npad, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     int r = check_common(Tq, Tk, H, npad);
     if (r) return r;
     if (Dh <= 0 || Dh > 256) return fail(KILN_EUNSUPPORTED, "exact attention: head size %d outside 1..256", Dh);
@@ -395,6 +401,7 @@ size_t kiln_attn_fwd_f16in_workspace_bytes(int B, int Tk, int H) {
 int kiln_attn_fwd_f16in(void* out, int out_dtype, int ldo, long long bso, const uint16_t* q, int ldq, long long bsq,
                         const uint16_t* k, int ldk, long long bsk, const uint16_t* v, int ldv, long long bsv, int B,
                         int Tq, int Tk, int H, int npad, void* workspace, size_t ws_bytes, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     if (out_dtype != KILN_F32 && out_dtype != KILN_F16) return fail(KILN_EINVAL, "out_dtype %d", out_dtype);
     int r = check_common(Tq, Tk, H, npad);
     if (r) return r;
@@ -427,6 +434,7 @@ int kiln_dit_self_attn_fused(void* out, int out_dtype, int ldo, const void* q, c
                              int in_dtype, int ld, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
                              const float* rope_cos, const float* rope_sin, int B, int T, int H, void* workspace,
                              size_t ws_bytes, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     if ((in_dtype != KILN_F32 && in_dtype != KILN_F16) || (out_dtype != KILN_F32 && out_dtype != KILN_F16))
         return fail(KILN_EINVAL, "dtype");
     if (B <= 0 || T <= 0 || H <= 0) return fail(KILN_EINVAL, "bad sizes B=%d T=%d H=%d", B, T, H);
@@ -496,7 +504,10 @@ int kiln_dit_self_attn_x16(void* out, int out_dtype, int ldo, const uint16_t* x1
     g.eps = eps;
     g.rcos = rope_cos;
     g.rsin = rope_sin;
-    rc = hip_check(kiln::launch_gemm16(g, s), "qkv projection launch");
+    {
+        kiln::prof::Scope prof_("gemm_tc16", s);
+        rc = hip_check(kiln::launch_gemm16(g, s), "qkv projection launch");
+    }
     if (rc) return rc;
     const DT od = (DT)out_dtype;
     const size_t osz = od == DT::F16 ? 2 : 4;
@@ -512,6 +523,7 @@ int kiln_dit_self_attn_x16(void* out, int out_dtype, int ldo, const uint16_t* x1
     a.q_prescaled = true;
     a.ksplit = kiln::attn_key_split(B, T, T, H);
     a.part = a.ksplit > 1 ? part : nullptr;
+    kiln::prof::Scope prof_("attention", s);
     return hip_check(kiln::launch_attn_fwd(a, s), "attn_fwd launch");
 }
 
@@ -562,6 +574,7 @@ int kiln_cross_attn_nag(void* out, void* out_neg, int out_dtype, int ldo, const 
                         const uint16_t* q_norm_w, float eps, int B, int T, int H, const uint16_t* const* kvp,
                         const int* Lk, const int* npad, const uint16_t* kvp_neg, int Lk_neg, int npad_neg,
                         float nag_scale, float nag_tau, float nag_alpha, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     return cross_attn_impl(out, out_neg, out_dtype, ldo, q, in_dtype, ldq, q_norm_w, eps, B, T, H, kvp, Lk, npad,
                            kvp_neg, Lk_neg, npad_neg, nag_scale, nag_tau, nag_alpha, false, stream);
 }
@@ -593,14 +606,20 @@ int kiln_dit_cross_attn_x16(void* out, void* out_neg, int out_dtype, int ldo, co
     g.qw = q_norm_w;
     g.kw = q_norm_w;
     g.eps = eps;
-    int rc = hip_check(kiln::launch_gemm16(g, (hipStream_t)stream), "cross-Q projection launch");
+    int rc;
+    {
+        kiln::prof::Scope prof_("gemm_tc16", (hipStream_t)stream);
+        rc = hip_check(kiln::launch_gemm16(g, (hipStream_t)stream), "cross-Q projection launch");
+    }
     if (rc) return rc;
+    kiln::prof::Scope prof_("attention", (hipStream_t)stream);
     return cross_attn_impl(out, out_neg, out_dtype, ldo, q16, KILN_F16, D, nullptr, eps, B, T, H, kvp, Lk, npad, kvp_neg,
                            Lk_neg, npad_neg, nag_scale, nag_tau, nag_alpha, true, stream);
 }
 
 int kiln_rmsnorm_rows(float* y, const float* x, const uint16_t* w_bf16, int rows, int dim, float eps,
                       kiln_stream_t stream) {
+    kiln::prof::Scope prof_("norm", (hipStream_t)stream);
     if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes");
     if (rows && (!y || !x)) return fail(KILN_EINVAL, "null pointer");
     return hip_check(kiln::launch_rmsnorm_rows(y, x, w_bf16, rows, dim, eps, (hipStream_t)stream), "rmsnorm launch");
@@ -608,6 +627,7 @@ int kiln_rmsnorm_rows(float* y, const float* x, const uint16_t* w_bf16, int rows
 
 int kiln_layernorm_mod(float* y, const float* x, const float* scale, const float* shift, int rows, int dim, float eps,
                        kiln_stream_t stream) {
+    kiln::prof::Scope prof_("layernorm", (hipStream_t)stream);
     if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes rows=%d dim=%d", rows, dim);
     if (rows && (!y || !x || !scale || !shift)) return fail(KILN_EINVAL, "null pointer");
     return hip_check(kiln::launch_layernorm_mod(y, kiln::DT::F32, x, scale, shift, rows, dim, eps, (hipStream_t)stream),
@@ -616,6 +636,7 @@ int kiln_layernorm_mod(float* y, const float* x, const float* scale, const float
 
 int kiln_layernorm_mod16(uint16_t* y, const float* x, const float* scale, const float* shift, int rows, int dim,
                          float eps, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("layernorm", (hipStream_t)stream);
     if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes rows=%d dim=%d", rows, dim);
     if (rows && (!y || !x || !scale || !shift)) return fail(KILN_EINVAL, "null pointer");
     return hip_check(kiln::launch_layernorm_mod(y, kiln::DT::F16, x, scale, shift, rows, dim, eps, (hipStream_t)stream),
@@ -623,6 +644,7 @@ int kiln_layernorm_mod16(uint16_t* y, const float* x, const float* scale, const 
 }
 
 int kiln_add_gated(float* x, const float* y, const float* gate, int rows, int dim, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (rows < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes rows=%d dim=%d", rows, dim);
     if (rows && (!x || !y)) return fail(KILN_EINVAL, "null pointer");
     return hip_check(kiln::launch_add_gated(x, y, gate, rows, dim, (hipStream_t)stream), "add_gated launch");
@@ -664,12 +686,14 @@ static int linear16_impl(const char* fn, void* y, int ldy, const uint16_t* x16, 
 
 int kiln_linear16(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* w16, int rows, int cols, int epi,
                   const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("gemm_tc16", (hipStream_t)stream);
     return linear16_impl("linear16", y, ldy, x16, T, w16, rows, cols, epi, gate, beta, a2, w2, k2, false, stream);
 }
 
 int kiln_linear16_prepped(void* y, int ldy, const uint16_t* x16, int T, const uint16_t* wp, int rows, int cols,
                           int epi, const float* gate, float beta, const uint16_t* a2, const uint16_t* w2, int k2,
                           kiln_stream_t stream) {
+    kiln::prof::Scope prof_("gemm_tc16", (hipStream_t)stream);
     return linear16_impl("linear16_prepped", y, ldy, x16, T, wp, rows, cols, epi, gate, beta, a2, w2, k2, true, stream);
 }
 
@@ -680,6 +704,7 @@ size_t kiln_linear16_prepped_weight_bytes(int rows, int cols) {
 
 int kiln_linear16_prepare_weight(uint16_t* wp, const uint16_t* w, int rows, int cols, int src_bf16,
                                  kiln_stream_t stream) {
+    kiln::prof::Scope prof_("w->f16", (hipStream_t)stream);
     if (rows <= 0 || cols <= 0) return fail(KILN_EINVAL, "linear16_prepare_weight: bad sizes rows=%d cols=%d", rows, cols);
     if (rows % 128 || cols % 32)
         return fail(KILN_EUNSUPPORTED, "linear16_prepare_weight: needs rows %% 128 == 0, cols %% 32 == 0 (rows=%d cols=%d)",
@@ -695,6 +720,7 @@ int kiln_linear16_prepare_weight(uint16_t* wp, const uint16_t* w, int rows, int 
 
 int kiln_matvec_bf16(float* y, const uint16_t* w_bf16, const float* x, const float* add, int rows, int cols,
                      kiln_stream_t stream) {
+    kiln::prof::Scope prof_("matvec", (hipStream_t)stream);
     if (rows < 0 || cols <= 0) return fail(KILN_EINVAL, "matvec: bad sizes rows=%d cols=%d", rows, cols);
     if (rows && (!y || !w_bf16 || !x)) return fail(KILN_EINVAL, "matvec: null pointer");
     if (!rows) return KILN_OK;
@@ -703,6 +729,7 @@ int kiln_matvec_bf16(float* y, const uint16_t* w_bf16, const float* x, const flo
 
 int kiln_matvec_bf16_grouped(float* y, const uint16_t* w_bf16, const float* x, const float* add, int groups, int rows,
                              int cols, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("matvec", (hipStream_t)stream);
     if (groups < 0 || rows < 0 || cols <= 0 || (long)groups * rows > (1L << 30))
         return fail(KILN_EINVAL, "matvec_grouped: bad sizes groups=%d rows=%d cols=%d", groups, rows, cols);
     if (!groups || !rows) return KILN_OK;
@@ -712,18 +739,21 @@ int kiln_matvec_bf16_grouped(float* y, const uint16_t* w_bf16, const float* x, c
 }
 
 int kiln_silu(float* y, const float* x, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!y || !x)) return fail(KILN_EINVAL, "silu: null pointer");
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_silu(y, x, n, (hipStream_t)stream), "silu launch");
 }
 
 int kiln_patchify(float* tok, const float* latent, int Hl, int Wl, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (Hl <= 0 || Wl <= 0 || Hl % 2 || Wl % 2) return fail(KILN_EINVAL, "patchify: Hl=%d Wl=%d (even, > 0)", Hl, Wl);
     if (!tok || !latent) return fail(KILN_EINVAL, "patchify: null pointer");
     return hip_check(kiln::launch_patchify(tok, latent, Hl, Wl, (hipStream_t)stream), "patchify launch");
 }
 
 int kiln_unpatchify(float* latent, const float* tok, int ldt, int Hl, int Wl, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (Hl <= 0 || Wl <= 0 || Hl % 2 || Wl % 2 || ldt < 64)
         return fail(KILN_EINVAL, "unpatchify: Hl=%d Wl=%d ldt=%d", Hl, Wl, ldt);
     if (!tok || !latent) return fail(KILN_EINVAL, "unpatchify: null pointer");
@@ -732,6 +762,7 @@ int kiln_unpatchify(float* latent, const float* tok, int ldt, int Hl, int Wl, ki
 
 int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* w_bf16, int T, int rows, int cols,
                     kiln_stream_t stream) {
+    kiln::prof::Scope prof_("gemm_fp32", (hipStream_t)stream);
     if (T < 0 || rows <= 0 || cols <= 0 || ldy < rows || ldx < cols)
         return fail(KILN_EINVAL, "linear_f32: bad sizes T=%d rows=%d cols=%d ldy=%d ldx=%d", T, rows, cols, ldy, ldx);
     if (!T) return KILN_OK;
@@ -741,24 +772,28 @@ int kiln_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* 
 }
 
 int kiln_cfg_combine(float* v, const float* vn, float cfg, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!v || !vn)) return fail(KILN_EINVAL, "cfg_combine: null pointer");
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_cfg_combine(v, vn, cfg, n, (hipStream_t)stream), "cfg_combine launch");
 }
 
 int kiln_pad_circular(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (Hs <= 0 || Ws <= 0 || Hd <= 0 || Wd <= 0) return fail(KILN_EINVAL, "pad_circular: bad sizes");
     if (!dst || !src) return fail(KILN_EINVAL, "pad_circular: null pointer");
     return hip_check(kiln::launch_pad_circular(dst, src, Hs, Ws, Hd, Wd, (hipStream_t)stream), "pad_circular launch");
 }
 
 int kiln_crop(float* dst, const float* src, int Hs, int Ws, int Hd, int Wd, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (Hs <= 0 || Ws <= 0 || Hd <= 0 || Wd <= 0 || Hd > Hs || Wd > Ws) return fail(KILN_EINVAL, "crop: bad sizes");
     if (!dst || !src) return fail(KILN_EINVAL, "crop: null pointer");
     return hip_check(kiln::launch_crop(dst, src, Hs, Ws, Hd, Wd, (hipStream_t)stream), "crop launch");
 }
 
 int kiln_fill_uniform_bf16(uint16_t* p, size_t n, uint64_t seed, float lo, float hi, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && !p) return fail(KILN_EINVAL, "fill_uniform_bf16: null pointer");
     if (!(lo <= hi)) return fail(KILN_EINVAL, "fill_uniform_bf16: lo > hi");
     if (!n) return KILN_OK;
@@ -766,12 +801,14 @@ int kiln_fill_uniform_bf16(uint16_t* p, size_t n, uint64_t seed, float lo, float
 }
 
 int kiln_sub(float* y, const float* a, const float* b, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!y || !a || !b)) return fail(KILN_EINVAL, "sub: null pointer");
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_sub(y, a, b, n, (hipStream_t)stream), "sub launch");
 }
 
 int kiln_rel_l1(const float* a, const float* b, size_t n, float* acc, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (!acc || (n && (!a || !b))) return fail(KILN_EINVAL, "rel_l1: null pointer");
     return hip_check(kiln::launch_rel_l1(a, b, n, acc, (hipStream_t)stream), "rel_l1 launch");
 }
@@ -783,6 +820,7 @@ int kiln_torch_randn(float* host_out, uint64_t seed, size_t n) {
 }
 
 int kiln_flow_start(float* x, const float* noise, const float* init, float sigma, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!x || !noise)) return fail(KILN_EINVAL, "flow_start: null pointer");
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_flow_start(x, noise, init, sigma, n, (hipStream_t)stream), "flow_start launch");
@@ -791,6 +829,7 @@ int kiln_flow_start(float* x, const float* noise, const float* init, float sigma
 int kiln_flow_ersde_step(float* x, const float* den, const float* old, float* oldd, const float* noise, float a,
                          float b, float c2, float inv2, float c3, float inv3, float cn, int stage, size_t n,
                          kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (stage < 1 || stage > 3) return fail(KILN_EINVAL, "flow_ersde_step: stage %d", stage);
     if (n && (!x || !den || (stage >= 2 && (!old || !oldd)))) return fail(KILN_EINVAL, "flow_ersde_step: null pointer");
     if (!n) return KILN_OK;
@@ -800,6 +839,7 @@ int kiln_flow_ersde_step(float* x, const float* den, const float* old, float* ol
 }
 
 int kiln_gelu(float* x, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && !x) return fail(KILN_EINVAL, "gelu: null pointer");
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_gelu(x, n, (hipStream_t)stream), "gelu launch");
@@ -807,6 +847,7 @@ int kiln_gelu(float* x, size_t n, kiln_stream_t stream) {
 
 int kiln_flow_inpaint_in(float* xin, const float* x, const float* noise, const float* init, const float* mask,
                          float sigma, int P, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (P < 0 || (P && (!xin || !x || !noise || !init || !mask))) return fail(KILN_EINVAL, "flow_inpaint_in: bad args");
     if (!P) return KILN_OK;
     return hip_check(kiln::launch_flow_inpaint_in(xin, x, noise, init, mask, sigma, P, (hipStream_t)stream),
@@ -815,6 +856,7 @@ int kiln_flow_inpaint_in(float* xin, const float* x, const float* noise, const f
 
 int kiln_flow_denoised_masked(float* den, const float* xin, const float* v, const float* init, const float* mask,
                               float sigma, int P, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (P < 0 || (P && (!den || !xin || !v || !init || !mask))) return fail(KILN_EINVAL, "flow_denoised_masked: bad args");
     if (!P) return KILN_OK;
     return hip_check(kiln::launch_flow_denoised_masked(den, xin, v, init, mask, sigma, P, (hipStream_t)stream),
@@ -822,6 +864,7 @@ int kiln_flow_denoised_masked(float* den, const float* xin, const float* v, cons
 }
 
 int kiln_flow_denoised(float* den, const float* x, const float* v, float sigma, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!den || !x || !v)) return fail(KILN_EINVAL, "flow_denoised: null pointer");
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_flow_denoised(den, x, v, sigma, n, (hipStream_t)stream), "flow_denoised launch");
@@ -829,12 +872,14 @@ int kiln_flow_denoised(float* den, const float* x, const float* v, float sigma, 
 
 int kiln_flow_update(float* x, const float* den, const float* old, float a, float b, float c, size_t n,
                      kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!x || !den)) return fail(KILN_EINVAL, "flow_update: null pointer");
     if (!n) return KILN_OK;
     return hip_check(kiln::launch_flow_update(x, den, old, a, b, c, n, (hipStream_t)stream), "flow_update launch");
 }
 
 int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!x || !v)) return fail(KILN_EINVAL, "flow_euler_step: null pointer");
     if (!(sigma > 0.f)) return fail(KILN_EINVAL, "flow_euler_step: sigma %g must be > 0", (double)sigma);
     if (!n) return KILN_OK;
@@ -842,6 +887,7 @@ int kiln_flow_euler_step(float* x, const float* v, float sigma, float sigma_next
 }
 
 int kiln_flow_euler_den(float* x, const float* den, float sigma, float sigma_next, size_t n, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("eltwise", (hipStream_t)stream);
     if (n && (!x || !den)) return fail(KILN_EINVAL, "flow_euler_den: null pointer");
     if (!(sigma > 0.f)) return fail(KILN_EINVAL, "flow_euler_den: sigma %g must be > 0", (double)sigma);
     if (!n) return KILN_OK;
@@ -850,6 +896,7 @@ int kiln_flow_euler_den(float* x, const float* den, float sigma, float sigma_nex
 }
 
 int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const float* sin_t, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("rope", (hipStream_t)stream);
     if (T < 0 || H <= 0 || Dh <= 0 || Dh % 2) return fail(KILN_EINVAL, "bad sizes");
     if (T && (!x || !cos_t || !sin_t)) return fail(KILN_EINVAL, "null pointer");
     return hip_check(kiln::launch_rope_half(x, T, H, Dh, cos_t, sin_t, (hipStream_t)stream), "rope launch");
@@ -857,6 +904,7 @@ int kiln_rope_half(float* x, int T, int H, int Dh, const float* cos_t, const flo
 
 int kiln_nag_combine(void* a, int lda, const void* an, int ldn, int dtype, int T, int dim, float s, float tau,
                      float alpha, kiln_stream_t stream) {
+    kiln::prof::Scope prof_("nag", (hipStream_t)stream);
     if (dtype != KILN_F32 && dtype != KILN_F16) return fail(KILN_EINVAL, "dtype %d", dtype);
     if (T < 0 || dim <= 0) return fail(KILN_EINVAL, "bad sizes");
     if (T && (!a || !an)) return fail(KILN_EINVAL, "null pointer");

@@ -27,3 +27,19 @@ int flash_self(void* out, DT od, int ldo, long long bso, const void* q, int ldq,
                size_t ws_bytes, hipStream_t stream);
 
 }  // namespace kiln::capi
+
+namespace kiln::prof {
+// A timed scope of one category on a stream (kiln_prof_enable / kiln_prof_report).
+class Scope {
+   public:
+    Scope(const char* name, hipStream_t s);
+    ~Scope();
+    Scope(const Scope&) = delete;
+    Scope& operator=(const Scope&) = delete;
+
+   private:
+    int slot_ = -1;
+    bool nested_ = false;
+    hipStream_t s_ = nullptr;
+};
+}  // namespace kiln::prof

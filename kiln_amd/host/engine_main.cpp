@@ -177,6 +177,7 @@ class Engine {
     void set_gpu_name(const std::string& n) { gpu_ = n; }
 
     void generate(const Job& j);
+    int bench(int W, int H);
 
    private:
     kiln::DitDims dims_;
@@ -316,11 +317,50 @@ void Engine::generate(const Job& j) {
     }
 }
 
+// --bench WxH (main.cpp:110-150): the warm time of one DiT forward of the CFG pair at W x H with NAG on the prompt
+// item, then its per-category GPU profile (kiln_prof_*), as log events
+int Engine::bench(int W, int H) {
+    const int Hl = H / 8, Wl = W / 8;
+    const size_t n = (size_t)16 * Hl * Wl;
+    std::vector<int> ids(24);
+    for (int i = 0; i < 24; i++) ids[i] = 1000 + 37 * i;
+    auto pos = condition(ids, false);
+    auto neg = condition({151643}, false);
+    auto nagc = condition({9, 8, 7}, false);
+    kiln::DeviceBuffer x(n * 4), o(2 * n * 4);
+    std::vector<float> h(n);
+    for (size_t i = 0; i < n; i++) h[i] = (float)((mix64(i) >> 40) * (1.0 / 16777216.0)) * 2.f - 1.f;
+    kiln::ck_hip(hipMemcpy(x.get(), h.data(), n * 4, hipMemcpyHostToDevice), "latent");
+    float* outs[2] = {o.get<float>(), o.get<float>() + n};
+    const kiln::CachedContext* cs[2] = {pos.get(), neg.get()};
+    kiln::NagParams nag;
+    nag.neg = nagc.get();
+    auto fwd = [&] { dit_.forward_batch(outs, x.get<float>(), Hl, Wl, 0.9f, cs, 2, nag); };
+    fwd();  // warm-up (arena, RoPE tables, code objects)
+    kiln::ck_hip(hipStreamSynchronize(s_), "bench");
+    const auto t0 = Clock::now();
+    for (int i = 0; i < 3; i++) fwd();
+    kiln::ck_hip(hipStreamSynchronize(s_), "bench");
+    char b[200];
+    snprintf(b, sizeof b, "DiT forward of the CFG pair at %dx%d (latent %dx%d): %.2f ms", W, H, Wl, Hl, ms_since(t0) / 3);
+    log_msg(b);
+    kiln::ck(kiln_prof_enable(1), "prof");
+    fwd();
+    std::vector<char> rep(1 << 14);
+    kiln::ck(kiln_prof_report(rep.data(), rep.size()), "prof report");
+    kiln::ck(kiln_prof_enable(0), "prof");
+    std::istringstream ss(rep.data());
+    std::string line;
+    while (std::getline(ss, line)) log_msg(line);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     int device = 0;
     uint64_t wseed = 1;
+    int bench_w = 0, bench_h = 0;
     kiln::DitDims dims;  // the 2B model: 28 blocks, 16 heads, 1024-wide contexts
     for (int i = 1; i < argc; i++) {
         const std::string a = argv[i];
@@ -331,8 +371,14 @@ int main(int argc, char** argv) {
             else if (a == "--heads") dims.heads = std::stoi(next());
             else if (a == "--ctx-dim") dims.ctx_dim = std::stoi(next());
             else if (a == "--weights-seed") wseed = std::stoull(next());
+            else if (a == "--bench") {
+                const std::string wh = next();
+                bench_w = std::stoi(wh);
+                bench_h = std::stoi(wh.substr(wh.find('x') + 1));
+            }
             else if (a == "--help") {
-                printf("kiln_engine [--device N] [--blocks 28] [--heads 16] [--ctx-dim 1024] [--weights-seed S]\n");
+                printf("kiln_engine [--device N] [--blocks 28] [--heads 16] [--ctx-dim 1024] [--weights-seed S] "
+                       "[--bench WxH]\n");
                 return 0;
             }
         } catch (const std::exception&) {
@@ -347,16 +393,24 @@ int main(int argc, char** argv) {
         hipDeviceProp_t prop;
         kiln::ck_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
         kiln::ck_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
-        log_msg(std::string("GPU: ") + prop.name + " (" + prop.gcnArchName + ", " +
+        log_msg(std::string("GPU: ") + (prop.name[0] ? prop.name : "AMD Instinct") + " (" + prop.gcnArchName + ", " +
                 std::to_string(prop.totalGlobalMem >> 30) + " GB): fp16 MFMA path ON");
         emit("{\"ev\":\"loading\",\"what\":\"dit\"}");
         E = std::make_unique<Engine>(dims, wseed, stream);
-        E->set_gpu_name(prop.name);
+        E->set_gpu_name(prop.name[0] ? std::string(prop.name) : std::string("AMD ") + prop.gcnArchName);
         log_msg("DiT: " + std::to_string(dims.blocks) + " blocks x " + std::to_string(dims.heads) +
                 " heads, random-init weights (seed " + std::to_string(wseed) + "); text encoder and VAE: stand-ins");
     } catch (const std::exception& e) {
         emit(std::string("{\"ev\":\"fatal\",\"msg\":") + kiln::json::quote(e.what()) + "}");
         return 1;
+    }
+    if (bench_w > 0 && bench_h > 0) {
+        try {
+            return E->bench(bench_w / 16 * 16, bench_h / 16 * 16);
+        } catch (const std::exception& e) {
+            log_msg(std::string("bench failed: ") + e.what());
+            return 1;
+        }
     }
     emit("{\"ev\":\"ready\",\"gpu\":" + kiln::json::quote(E->gpu_name()) + ",\"tc\":true,\"tc16\":true}");
 

@@ -461,3 +461,36 @@ def test_dit_sample_in_cpp_matches_the_python_driven_loop(gpu):
     d.sample(xn, cc[0], neg=cc[1], **kw)
     torch.cuda.synchronize()
     assert torch.equal(xo, xn) and not torch.equal(xo, x)
+
+
+def test_profiler_categories_of_a_forward(gpu):
+    """kiln_prof_* (the reference's ProfScope / prof_report, engine/src/kernels.cu:14-58): a profiled forward of
+    the CFG pair reports the attention, GEMM, LayerNorm, matvec and elementwise categories; nested entry points
+    are counted once (the category sum stays within the forward's own event-timed duration); a disabled profiler
+    records nothing."""
+    g = torch.Generator().manual_seed(39)
+    d, _, _ = _make_dit(g, 2)
+    cc = [d.cache_context(torch.randn(r, DCTX, generator=g).to(DEV), length=L) for r in REALS]
+    lat = torch.randn(16, 2 * Hp, 2 * Wp, generator=g).to(DEV)
+    outs = [torch.empty_like(lat) for _ in range(B)]
+    d.forward(outs, lat, 0.5, cc[:B], nag=dit.Nag(cc[2], *NAG))  # warm
+    kiln_amd.prof_enable(True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    d.forward(outs, lat, 0.5, cc[:B], nag=dit.Nag(cc[2], *NAG))
+    e1.record()
+    cats, text = kiln_amd.prof_report()
+    kiln_amd.prof_enable(False)
+    torch.cuda.synchronize()
+    print(text)
+    for c in ("attention", "gemm_tc16", "layernorm", "matvec", "gemm_fp32", "eltwise"):
+        assert c in cats and cats[c][1] > 0 and cats[c][0] > 0, (c, cats)
+    # 2 blocks: per block one self-attention and one cross-attention section, 3 LN16, 4 linear16 (O, O, MLP x 2) and
+    # the two projections inside the fused sections
+    assert cats["attention"][1] == 4 and cats["layernorm"][1] == 2 * 3 + 1 and cats["gemm_tc16"][1] == 2 * 6
+    total = sum(v[0] for v in cats.values())
+    assert total <= e0.elapsed_time(e1) * 1.05 + 0.05
+    kiln_amd.prof_enable(True)
+    kiln_amd.prof_enable(False)
+    cats, _ = kiln_amd.prof_report()
+    assert cats == {}

@@ -288,6 +288,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--main-only", action="store_true",
                     help="run only the config-4 attention kernel loop (for rocprofv3 runs)")
+    ap.add_argument("--call-only", action="store_true",
+                    help="run only the config-4 whole call (K/V prepare + attention) loop (for rocprofv3 runs)")
     ap.add_argument("--linear16-only", action="store_true",
                     help="run only the DiT-shape linear16 cases (for rocprofv3 runs)")
     ap.add_argument("--forward-only", action="store_true",
@@ -329,9 +331,10 @@ def main():
         return 0
 
     cfg4 = self_attn_case(torch, kiln_amd, 64, 64, 2, 4, dev)
-    if args.main_only:
-        ms = tm.run(cfg4["main"], args.steps, args.warmup)
-        log(f"k_attn_fwd config 4: {ms * 1e3:.1f} us  {cfg4['flop'] / ms / 1e9:.1f} TFLOP/s")
+    if args.main_only or args.call_only:
+        ms = tm.run(cfg4["main" if args.main_only else "step"], args.steps, args.warmup)
+        log(f"{'k_attn_fwd' if args.main_only else 'whole call'} config 4: {ms * 1e3:.1f} us  "
+            f"{cfg4['flop'] / ms / 1e9:.1f} TFLOP/s")
         return 0
 
     ms4 = tm.run(cfg4["step"], args.steps, args.warmup)

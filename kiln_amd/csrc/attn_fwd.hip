@@ -462,20 +462,24 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 
     using True = std::true_type;
     using False = std::false_type;
+    // Steps j = 0 .. nh-2 (each with a successor), then the last half tile. Only a ragged last half tile of the
+    // keys needs the masking step; every other step runs one of the two copies below (the unrolled pair or the
+    // single step), so no third copy of the step body, with its own register allocation, is inlined.
+    const bool ragged = (Tk & 31) != 0 && h0 + nh == nhall;
+    const int nplain = nh - 1 - (ragged && nh >= 2 ? 1 : 0);  // steps without masking: j = 0 .. nplain-1
     int j = 0;
-    for (; j + 1 < nh - 2; j += 2) {
+    for (; j + 1 < nplain; j += 2) {
         step(False{}, j, sc, sc2);
         step(False{}, j + 1, sc2, sc);
     }
-    if (j < nh - 2) {
+    if (j < nplain) {
         step(False{}, j, sc, sc2);
         j++;
 #pragma unroll
         for (int b = 0; b < QB; b++) sc[b] = sc2[b];
     }
-    if (nh >= 2) {
-        if ((Tk & 31) != 0 && h0 + nh == nhall) step(True{}, j, sc, sc2);
-        else step(False{}, j, sc, sc2);
+    if (ragged && nh >= 2) {
+        step(True{}, j, sc, sc2);
         j++;
 #pragma unroll
         for (int b = 0; b < QB; b++) sc[b] = sc2[b];

@@ -438,6 +438,15 @@ def main():
 
     cfgb = dit_forward_case(torch, kiln_amd, dev)
     ms_blk = tm.run(cfgb["step"], max(3, args.steps // 5), 1)
+    # the same forward's attention on the production path (QKV projection epilogue preparing K/V, 28 blocks of
+    # self-attention of the pair + cross-attention + NAG), from the library's per-category event timing
+    kiln_amd.prof_enable(True)
+    cfgb["step"]()
+    cats, _ = kiln_amd.prof_report()
+    kiln_amd.prof_enable(False)
+    ms5_fused = cats.get("attention", (float("nan"), 0))[0]
+    log(f"config 5, attention of the fused-path forward (profiler): {ms5_fused:.3f} ms over "
+        f"{cats.get('attention', (0, 0))[1]} calls; GEMMs {cats.get('gemm_tc16', (0, 0))[0]:.3f} ms")
     log(f"config 5, DiT forward of the CFG pair on the fp16 path (step tables, embed, 28 blocks, final layer): "
         f"{ms_blk:.3f} ms per step  {cfgb['flop'] / ms_blk / 1e9:.1f} TFLOP/s")
     cfgb_flop = cfgb["flop"]
@@ -445,11 +454,14 @@ def main():
     log(f"config 5, 8-step Euler sampling with CFG 4.5 + NAG (8 forwards of the CFG pair): {ms_s8:.1f} ms")
     del cfgb
 
-    traffic = None  # HBM bytes per launch of k_attn_fwd (config 4), from the committed rocprofv3 FETCH/WRITE runs
+    # HBM bytes per launch of k_attn_fwd (config 4): the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs, with the
+    # commit whose kernel they measured
+    traffic, traffic_commit = None, None
     tpath = os.path.join(ROOT, "profiles", "k_attn_fwd_config4_hbm_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("traffic_bytes")
+            tj = json.load(f)
+        traffic, traffic_commit = tj.get("traffic_bytes"), tj.get("commit")
 
     cpu = None
     if not args.no_cpu:
@@ -484,6 +496,7 @@ def main():
             "cross_nag_1536x512_ms_per_call": round(ms3, 5),
             "cross_nag_1536x512_tflops": round(tf3, 2),
             "dit_step_attention_ms": round(ms5, 4),
+            "dit_step_attention_ms_fused_path": round(ms5_fused, 4),
             "dit_step_workload": "config 5: 768x1152 (T=3456), B=2, 28 blocks x (self + cross L=512 + NAG)",
             "layernorm_mod16_us": round(ms_ln * 1e3, 2),
             "layernorm_mod16_tbps": round(ln_tbps, 3),
@@ -511,6 +524,8 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(tf4_main / PEAK_TFLOPS, 4),
             "traffic": traffic,
+            "traffic_source": "profiles/k_attn_fwd_config4_hbm_traffic.md",
+            "traffic_commit": traffic_commit,
         },
         "cpu_baseline": cpu,
     }

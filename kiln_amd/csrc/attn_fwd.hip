@@ -289,7 +289,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         const float x0 = fmaxf(fmaxf(a[0], a[1]), a[2]), x1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
         const float x2 = fmaxf(fmaxf(a[6], a[7]), a[8]), x3 = fmaxf(fmaxf(a[9], a[10]), a[11]);
         const float x4 = fmaxf(fmaxf(a[12], a[13]), a[14]);
-        return pair_max(fmaxf(fmaxf(fmaxf(x0, x1), x2), fmaxf(fmaxf(x3, x4), a[15])));
+        return fmaxf(fmaxf(fmaxf(x0, x1), x2), fmaxf(fmaxf(x3, x4), a[15]));
     };
 
     // prologue: half tiles 0 .. NS-2 in flight, then the Q tile loads (their latencies overlap); wait for
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     __builtin_amdgcn_s_barrier();
 
     floatx16 o[QB][4];
-    float m[QB], l[QB], mx[QB];
+    float m[QB], l[QB], l2[QB], mx[QB];  // row sum: two partial chains (l, l2), added in the epilogue
     floatx16 sc[QB], sc2[QB];  // S_j - m and S_{j+1} - m; the unrolled loop alternates their roles
     floatx16 mneg[QB];         // -m in every accumulator item: the first QK MFMA of a chain starts from it
 #pragma unroll
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         for (int db = 0; db < 4; db++)
 #pragma unroll
             for (int i = 0; i < 16; i++) o[b][db][i] = 0.f;
-        l[b] = 0.f;
+        l[b] = l2[b] = 0.f;
     }
     const half2v ones = {(_Float16)1.f, (_Float16)1.f};
 
@@ -333,8 +333,8 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 #pragma unroll
         for (int s = 0; s < 8; s++) sc[b] = mfma32(ka[s], qreg[b][s], sc[b]);
         if (Tk < 32) mask_half(0, Tk, hh, sc[b]);
-        m[b] = max16(sc[b]);  // the first half tile sets the running max
-        mx[b] = 0.f;          // max(S_j) - m
+        m[b] = pair_max(max16(sc[b]));  // the first half tile sets the running max (of both lanes of a query)
+        mx[b] = 0.f;  // max(S_j) - m over this lane's 16 keys of the row (its partner lane holds the other 16)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             sc[b][i] -= m[b];
@@ -349,18 +349,21 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 
     // the running max moves up by d: O and l scale by 2^-d, and S_j - m (cur) shifts by -d
     auto rescale = [&](int b, floatx16(&cur)[QB]) {
-        const float d = fmaxf(mx[b], 0.f);
+        // the rescale decision is wave-uniform (a ballot over every lane's own maximum), so the lane pair's
+        // common maximum is formed only here, on the rare path
+        const float d = fmaxf(pair_max(mx[b]), 0.f);
         const float corr = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
         for (int db = 0; db < 4; db++)
 #pragma unroll
             for (int i = 0; i < 16; i++) o[b][db][i] *= corr;
         l[b] *= corr;
+        l2[b] *= corr;
         m[b] += d;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             cur[b][i] -= d;
-            mneg[b][i] = -m[b];
+            mneg[b][i] -= d;
         }
     };
     auto need_rescale = [&]() {
@@ -398,9 +401,6 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 #pragma unroll
         for (int b = 0; b < QB; b++) sn[b] = mfma32(ka[0], qreg[b][0], mneg[b]);
         half8 pb[QB][2];
-        float la[QB], lb[QB];
-#pragma unroll
-        for (int b = 0; b < QB; b++) la[b] = lb[b] = 0.f;
 #pragma unroll
         for (int s = 0; s < 8; s++) {
 #pragma unroll
@@ -413,8 +413,8 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
                 if (s & 1) {  // row sum of the fp16-rounded P values the PV MFMA consumes
                     const half2v p0 = {pb[b][s / 4][(2 * s - 2) % 8], pb[b][s / 4][(2 * s - 1) % 8]};
                     const half2v p1 = {pb[b][s / 4][(2 * s) % 8], pb[b][s / 4][(2 * s + 1) % 8]};
-                    la[b] = __builtin_amdgcn_fdot2(p0, ones, la[b], false);
-                    lb[b] = __builtin_amdgcn_fdot2(p1, ones, lb[b], false);
+                    l[b] = __builtin_amdgcn_fdot2(p0, ones, l[b], false);
+                    l2[b] = __builtin_amdgcn_fdot2(p1, ones, l2[b], false);
                 }
             }
         }
@@ -453,7 +453,6 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
             for (int b = 0; b < QB; b++) o[b][db] = mfma32(vb[db], pb[b][1], o[b][db]);
 #pragma unroll
         for (int b = 0; b < QB; b++) {
-            l[b] += la[b] + lb[b];
             mx[b] = max16(sn[b]);
         }
         st = st1;
@@ -513,6 +512,8 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
         }
     }
     KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is released
+#pragma unroll
+    for (int b = 0; b < QB; b++) l[b] += l2[b];
 #pragma unroll
     for (int b = 0; b < QB; b++) {
         if (p.ksplit > 1) {  // partial result of this key range: unnormalized O, running max m, row sum l

@@ -232,15 +232,24 @@ def linear16_cases(torch, kiln_amd, tm, dev, steps, warmup):
 
 
 def cpu_model():
-    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    """The host CPU as /proc/cpuinfo names it (lscpu's "Model name"), with its family and model numbers: a
+    virtualized host may report only "AMD EPYC", and the family (26 = Zen 5, 25 = Zen 3/4) still dates it."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                k, _, v = ln.partition(":")
+                k = k.strip()
+                if k in ("model name", "cpu family", "model") and k not in info:
+                    info[k] = v.strip()
+                if len(info) == 3:
+                    break
     except OSError:
-        pass
-    return None
+        return None
+    if "model name" not in info:
+        return None
+    extra = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model") if k in info)
+    return f"{info['model name']} ({extra})" if extra else info["model name"]
 
 
 def cpu_baseline(case, target_s=10.0):

@@ -6,13 +6,14 @@
 // accumulator) instead of the reference's GeForce-specific fp16 partial sums.
 //
 // Design (gfx950, wave64):
-//  * workgroup = 4 waves x 32 query rows (BM = 128); K/V stream in tiles of 64 keys.
-//  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_f16: each lane then owns ONE
-//    query column and 32 of the tile's 64 keys, so the row max needs one v_permlane32_swap and the row
-//    sum none until the epilogue.
-//  * O^T = V^T P^T: P^T comes straight out of the S^T accumulator (no LDS round trip); V^T is the A
-//    operand, pre-permuted by the K/V prepare pass so that every LDS operand read of a wave is one
-//    contiguous, conflict-free 1 KB ds_read_b128.
+//  * workgroup = 4 waves x 32 query rows (BM = 128); K/V stream in half tiles of 32 keys.
+//  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (under the chip's power limit
+//    this shape sustains more flop/s than 32x32x16): a wave's 32 rows are two 16-column query blocks, and
+//    the four lanes n, n+16, n+32, n+48 of a column hold 8 of each half tile's 32 keys, so the row sum needs
+//    no cross-lane step until the epilogue and the row max one only when the running max moves.
+//  * O^T = V^T P^T: P^T comes straight out of the two S^T accumulators of a query block (no LDS round trip);
+//    V^T is the A operand, pre-permuted by the K/V prepare pass so that every LDS operand read of a wave is
+//    one contiguous, conflict-free 1 KB ds_read_b128, and each read feeds both query blocks.
 //  * K/V stream through a ring of LDS stages filled by buffer-form global->LDS DMA, several tiles ahead.
 //  * the VALU, not the matrix core, is the tighter budget (MFMA and VALU work of a step barely overlap), so
 //    per-step vector work is cut to the softmax itself: the QK accumulator starts from -m (no subtraction
@@ -72,8 +73,8 @@ __device__ __forceinline__ void store4<float>(float* dst, float a, float b, floa
     }
 }
 
-__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // ---- shared pieces of the two kernels ----
@@ -116,90 +117,105 @@ struct Chunk8<float> {
     __device__ __forceinline__ float operator[](int e) const { return e < 4 ? a[e] : b[e - 4]; }
 };
 
-// Q tile of one lane: query `row`, d chunks {16s + 8hh .. +8} for s = 0..7 (the B operands of S^T = K Q^T),
-// RMSNorm and RoPE applied in fp32, pre-scaled by log2(e)/sqrt(128), rounded once to fp16.
+// Q tile of one lane: query rows row[qb] (qb = 0, 1: the wave's two 16-row blocks), d chunks {32c + 8g .. +8}
+// for c = 0..3 (the B operands of S^T = K Q^T), RMSNorm and RoPE applied in fp32, pre-scaled by
+// log2(e)/sqrt(128), rounded once to fp16. The four lanes g = 0..3 of a query column hold its 128 dims.
 template <typename InT, bool QNORM, bool ROPE>
-__device__ __forceinline__ void load_q(const AttnParams& p, const void* q, int row, bool qin, int h, int hh,
-                                       half8 (&qreg)[8]) {
-    // Every load (Q row, RoPE rows, norm weights) is issued before any of them is used, unconditionally (rows
+__device__ __forceinline__ void load_q(const AttnParams& p, const void* q, const int (&row)[2], const bool (&qin)[2],
+                                       int h, int g, half8 (&qreg)[2][4]) {
+    // Every load (Q rows, RoPE rows, norm weights) is issued before any of them is used, unconditionally (rows
     // past Tq read row 0 and are zeroed afterwards): one memory round trip for the whole tile. A per-lane
     // branch around a load, or a conversion scheduled between loads, serializes them.
-    const int rr = qin ? row : 0;
-    const InT* qr = reinterpret_cast<const InT*>(q) + (size_t)rr * p.ldq + h * HD + 8 * hh;
-    Chunk8<InT> raw[8];
+    int rr[2];
+    Chunk8<InT> raw[2][4];
 #pragma unroll
-    for (int s = 0; s < 8; s++) raw[s].load(qr + 16 * s);
-    floatx4 cr[4][2], sr[4][2];
+    for (int qb = 0; qb < 2; qb++) {
+        rr[qb] = qin[qb] ? row[qb] : 0;
+        const InT* qr = reinterpret_cast<const InT*>(q) + (size_t)rr[qb] * p.ldq + h * HD + 8 * g;
+#pragma unroll
+        for (int c = 0; c < 4; c++) raw[qb][c].load(qr + 32 * c);
+    }
+    floatx4 cr[2][2][2], sr[2][2][2];  // [qb][c < 2][4-element half]: RoPE pairs (d, d + 64) = chunks (c, c + 2)
     if constexpr (ROPE) {
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const float* cp = p.rcos + (size_t)rr * 64 + 16 * s + 8 * hh;
-            const float* sp = p.rsin + (size_t)rr * 64 + 16 * s + 8 * hh;
-            cr[s][0] = *reinterpret_cast<const floatx4*>(cp);
-            cr[s][1] = *reinterpret_cast<const floatx4*>(cp + 4);
-            sr[s][0] = *reinterpret_cast<const floatx4*>(sp);
-            sr[s][1] = *reinterpret_cast<const floatx4*>(sp + 4);
-        }
+        for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const float* cp = p.rcos + (size_t)rr[qb] * 64 + 32 * c + 8 * g;
+                const float* sp = p.rsin + (size_t)rr[qb] * 64 + 32 * c + 8 * g;
+                cr[qb][c][0] = *reinterpret_cast<const floatx4*>(cp);
+                cr[qb][c][1] = *reinterpret_cast<const floatx4*>(cp + 4);
+                sr[qb][c][0] = *reinterpret_cast<const floatx4*>(sp);
+                sr[qb][c][1] = *reinterpret_cast<const floatx4*>(sp + 4);
+            }
     }
-    uint16_t wb[8][8];
+    uint16_t wb[4][8];
     if constexpr (QNORM) {
 #pragma unroll
-        for (int s = 0; s < 8; s++)
+        for (int c = 0; c < 4; c++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) wb[s][e] = p.qw[16 * s + 8 * hh + e];
+            for (int e = 0; e < 8; e++) wb[c][e] = p.qw[32 * c + 8 * g + e];
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    float x[8][8];
 #pragma unroll
-    for (int s = 0; s < 8; s++)
+    for (int qb = 0; qb < 2; qb++) {
+        float x[4][8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) x[s][e] = qin ? raw[s][e] : 0.f;
-    if constexpr (QNORM) {
-        float ss = 0.f;
+        for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int s = 0; s < 8; s++)
+            for (int e = 0; e < 8; e++) x[c][e] = qin[qb] ? raw[qb][c][e] : 0.f;
+        if constexpr (QNORM) {
+            float ss = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) ss += x[s][e] * x[s][e];
-        ss = pair_sum(ss);
-        const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
+            for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int s = 0; s < 8; s++)
+                for (int e = 0; e < 8; e++) ss += x[c][e] * x[c][e];
+            ss = quad_sum(ss);
+            const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[s][e] = x[s][e] * r * bf16_to_f32(wb[s][e]);
-    }
-    if constexpr (ROPE) {
+            for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+                for (int e = 0; e < 8; e++) x[c][e] = x[c][e] * r * bf16_to_f32(wb[c][e]);
+        }
+        if constexpr (ROPE) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float cs = cr[s][e / 4][e % 4], sn = sr[s][e / 4][e % 4];
-                const float a = x[s][e], b = x[s + 4][e];
-                x[s][e] = a * cs - b * sn;
-                x[s + 4][e] = b * cs + a * sn;
-            }
-    }
+            for (int c = 0; c < 2; c++)
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
+                for (int e = 0; e < 8; e++) {
+                    const float cs = cr[qb][c][e / 4][e % 4], sn = sr[qb][c][e / 4][e % 4];
+                    const float a = x[c][e], b = x[c + 2][e];
+                    x[c][e] = a * cs - b * sn;
+                    x[c + 2][e] = b * cs + a * sn;
+                }
+        }
 #pragma unroll
-        for (int e = 0; e < 8; e++) x[s][e] *= p.qscale;
-        qreg[s] = to_half8(x[s]);
+        for (int c = 0; c < 4; c++) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[c][e] *= p.qscale;
+            qreg[qb][c] = to_half8(x[c]);
+        }
     }
 }
 
-// accumulator item i of a 32-key half tile holds key 32*jh + 8*(i/4) + 4*hh + i%4
-__device__ __forceinline__ void mask_half(int jh, int Tk, int hh, floatx16& a) {
-    const int kbase = jh * 32 + 4 * hh;
+// accumulator item i of key block kb of a 32-key half tile holds key 32*jh + 16*kb + 4*g + i
+__device__ __forceinline__ void mask_half(int jh, int Tk, int g, floatx4 (&a)[2][2]) {
+    const int kbase = jh * 32 + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 16; i++)
-        if (kbase + 8 * (i / 4) + (i % 4) >= Tk) a[i] = -INFINITY;
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (kbase + 16 * kb + i >= Tk) a[kb][qb][i] = -INFINITY;
 }
 
-// full row sum (lane pair), npad zero keys (tcflash.cuh:136-147), normalize, store this lane's row
+// full row sum (four lanes), npad zero keys (tcflash.cuh:136-147), normalize, store this lane's 32 dims of
+// the row: O^T accumulator db holds d = 16*db + 4*g + i
 template <typename OutT>
-__device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, int row, bool qin, int h, int hh,
-                                         float m, float l, const floatx16 (&o)[4]) {
-    float lt = pair_sum(l);
+__device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, int row, bool qin, int h, int g,
+                                         float m, float l, const floatx4 (&o)[8]) {
+    float lt = quad_sum(l);
     float sc = 1.f;
     if (J.npad) {
         const float mn = fmaxf(m, 0.f);
@@ -208,52 +224,47 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
     }
     const float inv = sc / lt;
     if (!qin) return;
-    OutT* orow = reinterpret_cast<OutT*>(J.o) + (size_t)row * p.ldo + h * HD + 4 * hh;
+    OutT* orow = reinterpret_cast<OutT*>(J.o) + (size_t)row * p.ldo + h * HD + 4 * g;
     const bool pairs = p.store_pairs != 0;
 #pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            store4<OutT>(orow + db * 32 + 8 * g, o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
-                         o[db][4 * g + 3] * inv, pairs);
+    for (int db = 0; db < 8; db++)
+        store4<OutT>(orow + 16 * db, o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv, pairs);
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
 #define KILN_WAIT_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 0xF) | (0x7 << 4) | (0xF << 8) | (((N) >> 4) << 14))
 
 // ------------------------------------------------------------------------------------------------
-// The kernel. A wave owns QB query blocks of 32 rows, a workgroup NW waves (BM = NW * QB * 32 = 128
-// rows), two workgroups per CU. QB = 1: two waves per SIMD (64 rows per wave at one wave per SIMD measured
-// slower). NS = 5 ring stages.
+// The kernel. A wave owns two query blocks of 16 rows (32 rows), a workgroup NW = 4 waves (BM = 128 rows), two
+// workgroups per CU (two waves per SIMD). NS = 5 ring stages. All products on v_mfma_f32_16x16x32_f16.
 //
 // Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB) through an NS-stage LDS ring filled by
 // direct global->LDS DMA (buffer_load_dwordx4 ... lds: no staging registers, no ds_write), NS-2 half
-// tiles ahead of use.
+// tiles ahead of use. Per half tile a wave issues 16 QK MFMAs (2 key blocks x 2 query blocks x 4 d chunks) and
+// 16 PV MFMAs (8 d blocks x 2 query blocks); each 1 KB K or V operand read from LDS feeds both query blocks.
 //
-// Software pipeline, per half tile j (S_j - m and max(S_j) - m in registers, K_{j+1}[0,4) operands in
+// Software pipeline, per half tile j (S_j - m and max(S_j) - m in registers, K_{j+1} d chunks 0-1 in
 // registers, half tiles j .. j+NS-3 resident or in flight):
 //   [rare: rescale O, l, m]                                         (the only branch)
-//   K_{j+1}[4,8), V_j[t=0] reads | QK_{j+1} MFMAs interleaved with exp/cvt/row-sum of S_j |
-//   wait tile j+2, barrier | DMA tile j+NS-1 into the stage of tile j-1 | K_{j+2}[0,4), V_j[t=1] reads |
+//   K_{j+1} chunks 2-3, V_j[db 0-3] reads | QK_{j+1} MFMAs interleaved with exp/cvt/row-sum of S_j |
+//   wait tile j+2, barrier | DMA tile j+NS-1 into the stage of tile j-1 | K_{j+2} chunks 0-1, V_j[db 4-7] reads |
 //   PV_j MFMAs interleaved with max(S_{j+1})
 // Every read of a stage completes before the barrier that precedes its refill.
 // ------------------------------------------------------------------------------------------------
 // a scheduling fence: keeps the phases of a step in the order written and bounds the live registers
 #define KILN_FENCE() __builtin_amdgcn_sched_barrier(0)
 typedef __attribute__((address_space(3))) half8 lds_half8;
-constexpr int QB = 1, NW = 4, NTHR = NW * 64, BM = NW * QB * 32, NS = 5;
+constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = 5;
 constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
 constexpr int PART_FLOATS = BM * HD + 2 * BM;      // one key range's partial result of a query tile
 static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
-static_assert(NW * QB == 4, "two workgroups of four 32-row blocks per CU");
-
 
 template <typename InT, typename OutT, bool QNORM, bool ROPE>
-__global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {  // 2nd: waves per SIMD
+__global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 2nd: waves per SIMD
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];  // NS x 16 KB
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int hh = lane >> 5;
+    const int g = lane >> 4;  // 16-lane row of the wave: keys 4g..4g+3 of a key block, dims 8g.. of a d chunk
     Work W;
     if (!decode_work(p, W)) return;
     const AttnJob J = p.job[W.jb];
@@ -285,11 +296,10 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     auto kptr = [&](int stage) {
         return reinterpret_cast<const lds_half8*>((size_t)(lds_base + stage * HT_H * 2 + lane * 16));
     };
-    auto max16 = [](const floatx16& a) {
-        const float x0 = fmaxf(fmaxf(a[0], a[1]), a[2]), x1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
-        const float x2 = fmaxf(fmaxf(a[6], a[7]), a[8]), x3 = fmaxf(fmaxf(a[9], a[10]), a[11]);
-        const float x4 = fmaxf(fmaxf(a[12], a[13]), a[14]);
-        return fmaxf(fmaxf(fmaxf(x0, x1), x2), fmaxf(fmaxf(x3, x4), a[15]));
+    // max over this lane's 8 keys of one query column (its two key-block accumulators)
+    auto max8 = [](const floatx4& a, const floatx4& b) {
+        const float x0 = fmaxf(fmaxf(a[0], a[1]), a[2]), x1 = fmaxf(fmaxf(a[3], b[0]), b[1]);
+        return fmaxf(fmaxf(x0, x1), fmaxf(b[2], b[3]));
     };
 
     // prologue: half tiles 0 .. NS-2 in flight, then the Q tile loads (their latencies overlap); wait for
@@ -297,48 +307,52 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
 #pragma unroll
     for (int i = 0; i < NS - 1; i++) dma(min(i, nh - 1), i);
     __builtin_amdgcn_sched_barrier(0);
-    int row[QB];
-    bool qin[QB];
-    half8 qreg[QB][8];
+    int row[2];
+    bool qin[2];
+    half8 qreg[2][4];
 #pragma unroll
-    for (int b = 0; b < QB; b++) {
-        row[b] = W.qt * BM + (wv * QB + b) * 32 + (lane & 31);
-        qin[b] = row[b] < p.Tq;
-        load_q<InT, QNORM, ROPE>(p, J.q, row[b], qin[b], W.h, hh, qreg[b]);
+    for (int qb = 0; qb < 2; qb++) {
+        row[qb] = W.qt * BM + wv * 32 + 16 * qb + (lane & 15);
+        qin[qb] = row[qb] < p.Tq;
     }
+    load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, g, qreg);
     KILN_WAIT_VMCNT((NS - 3) * DMA_PER_HT);
     __builtin_amdgcn_s_barrier();
 
-    floatx16 o[QB][4];
-    float m[QB], l[QB], l2[QB], mx[QB];  // row sum: two partial chains (l, l2), added in the epilogue
-    floatx16 sc[QB], sc2[QB];  // S_j - m and S_{j+1} - m; the unrolled loop alternates their roles
-    floatx16 mneg[QB];         // -m in every accumulator item: the first QK MFMA of a chain starts from it
+    floatx4 o[2][8];  // O^T per query block: d block db holds d = 16*db + 4g + i
+    float m[2], l[2], mx[2];
+    floatx4 sc[2][2], sc2[2][2];  // [key block][query block]: S_j - m and S_{j+1} - m; the unrolled loop
+                                  // alternates their roles
+    floatx4 mneg[2];              // -m in every item: the first QK MFMA of a chain starts from it
 #pragma unroll
-    for (int b = 0; b < QB; b++) {
+    for (int qb = 0; qb < 2; qb++) {
 #pragma unroll
-        for (int db = 0; db < 4; db++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[b][db][i] = 0.f;
-        l[b] = l2[b] = 0.f;
+        for (int db = 0; db < 8; db++) o[qb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+        l[qb] = 0.f;
     }
     const half2v ones = {(_Float16)1.f, (_Float16)1.f};
 
-    half8 ka[8];  // K operands: [0,4) of the next QK chains are read a phase ahead of [4,8)
+    half8 ka[8];  // K operands s = 2c + kb: d chunks 0-1 (s < 4) of the next QK chains are read a phase ahead
 #pragma unroll
     for (int s = 0; s < 8; s++) ka[s] = kptr(0)[s * 64];
 #pragma unroll
-    for (int b = 0; b < QB; b++) {
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) sc[b][i] = 0.f;
+        for (int qb = 0; qb < 2; qb++) sc[kb][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 8; s++) sc[b] = mfma32(ka[s], qreg[b][s], sc[b]);
-        if (Tk < 32) mask_half(0, Tk, hh, sc[b]);
-        m[b] = pair_max(max16(sc[b]));  // the first half tile sets the running max (of both lanes of a query)
-        mx[b] = 0.f;  // max(S_j) - m over this lane's 16 keys of the row (its partner lane holds the other 16)
+    for (int s = 0; s < 8; s++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            sc[b][i] -= m[b];
-            mneg[b][i] = -m[b];
+        for (int qb = 0; qb < 2; qb++) sc[s & 1][qb] = mfma16(ka[s], qreg[qb][s >> 1], sc[s & 1][qb]);
+    if (Tk < 32) mask_half(0, Tk, g, sc);
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        m[qb] = quad_max(max8(sc[0][qb], sc[1][qb]));  // the first half tile sets the running max of the row
+        mx[qb] = 0.f;  // max(S_j) - m over this lane's 8 keys of the row (three other lanes hold the rest)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            sc[0][qb][i] -= m[qb];
+            sc[1][qb][i] -= m[qb];
+            mneg[qb][i] = -m[qb];
         }
     }
 #pragma unroll
@@ -348,40 +362,36 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 
     // the running max moves up by d: O and l scale by 2^-d, and S_j - m (cur) shifts by -d
-    auto rescale = [&](int b, floatx16(&cur)[QB]) {
-        // the rescale decision is wave-uniform (a ballot over every lane's own maximum), so the lane pair's
-        // common maximum is formed only here, on the rare path
-        const float d = fmaxf(pair_max(mx[b]), 0.f);
-        const float corr = __builtin_amdgcn_exp2f(-d);
+    auto rescale = [&](floatx4(&cur)[2][2]) {
 #pragma unroll
-        for (int db = 0; db < 4; db++)
+        for (int qb = 0; qb < 2; qb++) {
+            // the rescale decision is wave-uniform (a ballot over every lane's own maximum), so the row's
+            // common maximum over its four lanes is formed only here, on the rare path
+            const float d = fmaxf(quad_max(mx[qb]), 0.f);
+            const float corr = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
-            for (int i = 0; i < 16; i++) o[b][db][i] *= corr;
-        l[b] *= corr;
-        l2[b] *= corr;
-        m[b] += d;
+            for (int db = 0; db < 8; db++) o[qb][db] *= corr;
+            l[qb] *= corr;
+            m[qb] += d;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            cur[b][i] -= d;
-            mneg[b][i] -= d;
+            for (int i = 0; i < 4; i++) {
+                cur[0][qb][i] -= d;
+                cur[1][qb][i] -= d;
+                mneg[qb][i] -= d;
+            }
         }
     };
     auto need_rescale = [&]() {
-        bool need = false;
-#pragma unroll
-        for (int b = 0; b < QB; b++) need |= mx[b] > RESCALE_TH;
+        const bool need = fmaxf(mx[0], mx[1]) > RESCALE_TH;
         return __builtin_amdgcn_ballot_w64(need) != 0;
     };
 
     int st = 0;        // stage of half tile j
     int st2 = NS - 1;  // stage that receives half tile j+NS-1
     // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
-    auto step = [&](auto maskn_tag, int j, floatx16 (&cur)[QB], floatx16 (&sn)[QB]) {
+    auto step = [&](auto maskn_tag, int j, floatx4 (&cur)[2][2], floatx4 (&sn)[2][2]) {
         constexpr bool MASKN = decltype(maskn_tag)::value;
-        if (need_rescale()) {  // lazy rescale (rare)
-#pragma unroll
-            for (int b = 0; b < QB; b++) rescale(b, cur);
-        }
+        if (need_rescale()) rescale(cur);  // lazy rescale (rare)
         const int st1 = st == NS - 1 ? 0 : st + 1;
         half8 va[4];
         {
@@ -390,33 +400,27 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
             for (int s = 4; s < 8; s++) ka[s] = kp[s * 64];
             const lds_half8* vp = kptr(st) + 32 * HD / 8;
 #pragma unroll
-            for (int g = 0; g < 4; g++) va[g] = vp[g * 64];
+            for (int db = 0; db < 4; db++) va[db] = vp[db * 64];
         }
         KILN_FENCE();
 
         // the softmax phase issues at a raised wave priority: when both waves of a SIMD are ready, the one with
-        // exp/convert work to interleave goes first (config 2: -2%, config 4: -0.3%)
+        // exp/convert work to interleave goes first
         __builtin_amdgcn_s_setprio(1);
-        // S_{j+1} on the matrix cores while the VALU turns S_j into P_j
-#pragma unroll
-        for (int b = 0; b < QB; b++) sn[b] = mfma32(ka[0], qreg[b][0], mneg[b]);
-        half8 pb[QB][2];
+        // S_{j+1} on the matrix cores while the VALU turns S_j into P_j: MFMA pair s (d chunk s/2, key block
+        // s%2, both query blocks) with P values 2s, 2s+1 (query block s/4, B-operand elements (2s)%8, +1)
+        half8 pb[2];
 #pragma unroll
         for (int s = 0; s < 8; s++) {
 #pragma unroll
-            for (int b = 0; b < QB; b++) {
-                if (s > 0) sn[b] = mfma32(ka[s], qreg[b][s], sn[b]);
-                const float e0 = __builtin_amdgcn_exp2f(cur[b][2 * s]);
-                const float e1 = __builtin_amdgcn_exp2f(cur[b][2 * s + 1]);
-                pb[b][s / 4][(2 * s) % 8] = (_Float16)e0;
-                pb[b][s / 4][(2 * s + 1) % 8] = (_Float16)e1;
-                if (s & 1) {  // row sum of the fp16-rounded P values the PV MFMA consumes
-                    const half2v p0 = {pb[b][s / 4][(2 * s - 2) % 8], pb[b][s / 4][(2 * s - 1) % 8]};
-                    const half2v p1 = {pb[b][s / 4][(2 * s) % 8], pb[b][s / 4][(2 * s + 1) % 8]};
-                    l[b] = __builtin_amdgcn_fdot2(p0, ones, l[b], false);
-                    l2[b] = __builtin_amdgcn_fdot2(p1, ones, l2[b], false);
-                }
-            }
+            for (int qb = 0; qb < 2; qb++)
+                sn[s & 1][qb] = mfma16(ka[s], qreg[qb][s >> 1], s < 2 ? mneg[qb] : sn[s & 1][qb]);
+            const int qb = s >> 2, e = (2 * s) % 8, kb = e / 4, i = e % 4;
+            pb[qb][e] = (_Float16)__builtin_amdgcn_exp2f(cur[kb][qb][i]);
+            pb[qb][e + 1] = (_Float16)__builtin_amdgcn_exp2f(cur[kb][qb][i + 1]);
+            // row sum of the fp16-rounded P values the PV MFMA consumes
+            const half2v pr = {pb[qb][e], pb[qb][e + 1]};
+            l[qb] = __builtin_amdgcn_fdot2(pr, ones, l[qb], false);
         }
         KILN_FENCE();
 
@@ -435,26 +439,22 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
             for (int s = 0; s < 4; s++) ka[s] = kp[s * 64];
             const lds_half8* vp = kptr(st) + 32 * HD / 8 + 4 * 64;
 #pragma unroll
-            for (int g = 0; g < 4; g++) vb[g] = vp[g * 64];
+            for (int db = 0; db < 4; db++) vb[db] = vp[db * 64];
         }
         KILN_FENCE();
 
-#pragma unroll
-        for (int b = 0; b < QB; b++)
-            if constexpr (MASKN) mask_half(h0 + j + 1, Tk, hh, sn[b]);
+        if constexpr (MASKN) mask_half(h0 + j + 1, Tk, g, sn);
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int db = 0; db < 4; db++)
 #pragma unroll
-            for (int b = 0; b < QB; b++) o[b][db] = mfma32(va[db], pb[b][0], o[b][db]);
+            for (int qb = 0; qb < 2; qb++) o[qb][db] = mfma16(va[db], pb[qb], o[qb][db]);
 #pragma unroll
         for (int db = 0; db < 4; db++)
 #pragma unroll
-            for (int b = 0; b < QB; b++) o[b][db] = mfma32(vb[db], pb[b][1], o[b][db]);
+            for (int qb = 0; qb < 2; qb++) o[qb][db + 4] = mfma16(vb[db], pb[qb], o[qb][db + 4]);
 #pragma unroll
-        for (int b = 0; b < QB; b++) {
-            mx[b] = max16(sn[b]);
-        }
+        for (int qb = 0; qb < 2; qb++) mx[qb] = max8(sn[0][qb], sn[1][qb]);
         st = st1;
         KILN_FENCE();
     };
@@ -466,6 +466,12 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     // single step), so no third copy of the step body, with its own register allocation, is inlined.
     const bool ragged = (Tk & 31) != 0 && h0 + nh == nhall;
     const int nplain = nh - 1 - (ragged && nh >= 2 ? 1 : 0);  // steps without masking: j = 0 .. nplain-1
+    auto copy_s = [&]() {
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) sc[kb][qb] = sc2[kb][qb];
+    };
     int j = 0;
     for (; j + 1 < nplain; j += 2) {
         step(False{}, j, sc, sc2);
@@ -474,63 +480,48 @@ __global__ __launch_bounds__(NTHR, 2 / QB) void k_attn_fwd(const AttnParams p) {
     if (j < nplain) {
         step(False{}, j, sc, sc2);
         j++;
-#pragma unroll
-        for (int b = 0; b < QB; b++) sc[b] = sc2[b];
+        copy_s();
     }
     if (ragged && nh >= 2) {
         step(True{}, j, sc, sc2);
         j++;
-#pragma unroll
-        for (int b = 0; b < QB; b++) sc[b] = sc2[b];
+        copy_s();
     }
     // last half tile: no successor
-    if (need_rescale()) {
-#pragma unroll
-        for (int b = 0; b < QB; b++) rescale(b, sc);
-    }
+    if (need_rescale()) rescale(sc);
     {
         half8 va[8];
         const lds_half8* vp = kptr(st) + 32 * HD / 8;
 #pragma unroll
-        for (int g = 0; g < 8; g++) va[g] = vp[g * 64];
+        for (int db = 0; db < 8; db++) va[db] = vp[db * 64];
 #pragma unroll
-        for (int b = 0; b < QB; b++) {
-            half8 pb[2];
+        for (int qb = 0; qb < 2; qb++) {
+            half8 pb;
 #pragma unroll
-            for (int i = 0; i < 16; i++) pb[i / 8][i % 8] = (_Float16)__builtin_amdgcn_exp2f(sc[b][i]);
+            for (int e = 0; e < 8; e++) pb[e] = (_Float16)__builtin_amdgcn_exp2f(sc[e / 4][qb][e % 4]);
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int e = 0; e < 8; e += 2) {
+                const half2v pr = {pb[e], pb[e + 1]};
+                l[qb] = __builtin_amdgcn_fdot2(pr, ones, l[qb], false);
+            }
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const half2v pr = {pb[t][2 * e], pb[t][2 * e + 1]};
-                    l[b] = __builtin_amdgcn_fdot2(pr, ones, l[b], false);
-                }
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int db = 0; db < 4; db++) o[b][db] = mfma32(va[t * 4 + db], pb[t], o[b][db]);
+            for (int db = 0; db < 8; db++) o[qb][db] = mfma16(va[db], pb, o[qb][db]);
         }
     }
     KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is released
 #pragma unroll
-    for (int b = 0; b < QB; b++) l[b] += l2[b];
-#pragma unroll
-    for (int b = 0; b < QB; b++) {
+    for (int qb = 0; qb < 2; qb++) {
         if (p.ksplit > 1) {  // partial result of this key range: unnormalized O, running max m, row sum l
             const int unit = (W.jb * p.H + W.h) * p.qtiles + W.qt;
             float* po = p.part + (size_t)(unit * p.ksplit + W.ks) * PART_FLOATS;
-            const int r = (wv * QB + b) * 32 + (lane & 31);
-            float* prow = po + r * HD + 4 * hh;
+            const int r = wv * 32 + 16 * qb + (lane & 15);
+            float* prow = po + r * HD + 4 * g;
 #pragma unroll
-            for (int db = 0; db < 4; db++)
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                    *reinterpret_cast<floatx4*>(prow + db * 32 + 8 * g) =
-                        floatx4{o[b][db][4 * g], o[b][db][4 * g + 1], o[b][db][4 * g + 2], o[b][db][4 * g + 3]};
-            const float lt = pair_sum(l[b]);
-            if (hh == 0) *reinterpret_cast<float2*>(po + BM * HD + 2 * r) = make_float2(m[b], lt);
+            for (int db = 0; db < 8; db++) *reinterpret_cast<floatx4*>(prow + 16 * db) = o[qb][db];
+            const float lt = quad_sum(l[qb]);
+            if (g == 0) *reinterpret_cast<float2*>(po + BM * HD + 2 * r) = make_float2(m[qb], lt);
         } else {
-            epilogue<OutT>(p, J, row[b], qin[b], W.h, hh, m[b], l[b], o[b]);
+            epilogue<OutT>(p, J, row[qb], qin[qb], W.h, g, m[qb], l[qb], o[qb]);
         }
     }
 }
@@ -654,30 +645,29 @@ __global__ __launch_bounds__(256) void k_kv_prep(const PrepParams p) {
 #pragma unroll
             for (int cc = 0; cc < 2; cc++) {
                 const int ch = q8 + 8 * cc;  // 8-element chunk of the row: d = 8 ch
-                *reinterpret_cast<half8*>(dst + kv_k_off(c, ch >> 1, kk + 32 * (ch & 1))) = to_half8(x[cc]);
+                *reinterpret_cast<half8*>(dst + kv_k_el(c, kk, 8 * ch)) = to_half8(x[cc]);
             }
         }
         __syncthreads();
-        // V^T operand units (t, db, lane): 8 keys of one d. ds_read_b64_tr_b16 (gfx950) transposes within each
+        // V^T operand units (db, lane): 8 keys of one d. ds_read_b64_tr_b16 (gfx950) transposes within each
         // group of 16 lanes: source lane r supplies 4 halves of row r/4, and lane i receives element e of row
         // 4e + i/4, column i%4. Lane r pointing at vt[key0 + r/4][d0 + 4(r%4)] therefore leaves lane i holding
-        // vt[key0 + e][d0 + i], e = 0..3: four consecutive keys of its own d.
+        // vt[key0 + e][d0 + i], e = 0..3: four consecutive keys of its own d. Lane group g takes keys 4g.. of
+        // both key blocks (key0 = 4g and 16 + 4g); wave w the d blocks 2w and 2w + 1.
         {
-            const int w = tid >> 6, ln = tid & 63, t = w >> 1;
+            const int w = tid >> 6, ln = tid & 63;
             const int g = ln >> 4, i = ln & 15;
-            const int key0 = 16 * t + 4 * (g >> 1);
             typedef short s4 __attribute__((ext_vector_type(4)));
             typedef short s8 __attribute__((ext_vector_type(8)));
             typedef __attribute__((address_space(3))) s4 lds_s4;
 #pragma unroll
             for (int dd = 0; dd < 2; dd++) {
-                const int db = 2 * (w & 1) + dd;
-                const int d0 = 32 * db + 16 * (g & 1);
-                const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[key0 + (i >> 2)][d0 + 4 * (i & 3)]);
-                const s4 hi =
-                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[key0 + 8 + (i >> 2)][d0 + 4 * (i & 3)]);
+                const int db = 2 * w + dd;
+                const int d0 = 16 * db + 4 * (i & 3);
+                const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[4 * g + (i >> 2)][d0]);
+                const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)&vt[16 + 4 * g + (i >> 2)][d0]);
                 const s8 o = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                *reinterpret_cast<s8*>(dst + kv_v_off(c, t, db, ln)) = o;
+                *reinterpret_cast<s8*>(dst + kv_v_off(c, db, ln)) = o;
             }
         }
         if (jh + 1 < t1) {

@@ -126,7 +126,7 @@ __device__ __forceinline__ float gelu_erf(float v) {
 // per-row sum of squares over the head (own half + partner's, through LDS), scale by rsqrt(mean + eps) and the
 // bf16 weight, then RoPE, whose pairs (i, i + 64) are the same accumulator element of the two partner waves
 // (exchanged through LDS two row blocks at a time). Q is stored as fp16(q * qscale) rows, K and V in the
-// prepared K/V layout of their item (kv_k_off / kv_v_off).
+// prepared K/V layout of their item (kv_k_el / kv_v_el).
 template <int MB>
 __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)[NBW][MB], _Float16* lds, int m0,
                                              int n0, int wv, int wn, int wm, int lane) {
@@ -215,17 +215,11 @@ __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)
                     half4{(_Float16)(v[0] * p.qscale), (_Float16)(v[1] * p.qscale), (_Float16)(v[2] * p.qscale),
                           (_Float16)(v[3] * p.qscale)};
             } else if (region == 1) {
-                const int klane = k32 + 32 * ((d % 16) / 8);
-                *reinterpret_cast<half4*>(kv + kv_k_off(kc, d / 16, klane) + d % 8) =
+                *reinterpret_cast<half4*>(kv + kv_k_el(kc, k32, d)) =
                     half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
             } else {
-                // V_c [t][db][lane][j]: d = 32 db + lane % 32, key = 16 t + 8 (j / 4) + 4 (lane / 32) + j % 4
-                const int tt = k32 / 16, jj = 4 * ((k32 / 8) % 2) + k32 % 4, lh = (k32 / 4) % 2;
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int dd = d + e;
-                    kv[kv_v_off(kc, tt, dd / 32, dd % 32 + 32 * lh) + jj] = (_Float16)v[e];
-                }
+                for (int e = 0; e < 4; e++) kv[kv_v_el(kc, k32, d + e)] = (_Float16)v[e];
             }
         }
     }

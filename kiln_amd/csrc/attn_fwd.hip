@@ -236,7 +236,8 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 
 // ------------------------------------------------------------------------------------------------
 // The kernel. A wave owns two query blocks of 16 rows (32 rows), a workgroup NW = 4 waves (BM = 128 rows), two
-// workgroups per CU (two waves per SIMD). NS = 5 ring stages. All products on v_mfma_f32_16x16x32_f16.
+// workgroups per CU (two waves per SIMD). NS = 4 ring stages (64 KB of LDS per workgroup; five measured the same
+// on long units and slower on short ones, whose prologue fills the ring). All products on v_mfma_f32_16x16x32_f16.
 //
 // Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB) through an NS-stage LDS ring filled by
 // direct global->LDS DMA (buffer_load_dwordx4 ... lds: no staging registers, no ds_write), NS-2 half
@@ -254,8 +255,9 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 // a scheduling fence: keeps the phases of a step in the order written and bounds the live registers
 #define KILN_FENCE() __builtin_amdgcn_sched_barrier(0)
 typedef __attribute__((address_space(3))) half8 lds_half8;
-constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = 5;
+constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = 4;
 constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
+static_assert(DMA_PER_HT == 4, "a wave copies four 1 KB pieces of each half tile");
 constexpr int PART_FLOATS = BM * HD + 2 * BM;      // one key range's partial result of a query tile
 static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
 
@@ -283,14 +285,17 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
     // SGPR soffset, so a refill costs no vector instructions. The descriptor's range is the head's K/V block.
     const __amdgpu_buffer_rsrc_t kv_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(kvh), (short)0, (int)(kv_head_stride(Tk) * 2), 0x00020000 /* raw, CDNA */);
-    const uint32_t dma_off = (uint32_t)tid * 16;
+    // Wave w copies the contiguous 4 KB [4w, 4w + 4) KB of the half tile in four 1 KB pieces: one M0 (LDS base)
+    // and one soffset serve all four, the piece offset is the instruction's immediate (it applies to the global
+    // and the LDS address alike).
+    const uint32_t dma_off = (uint32_t)wv * (DMA_PER_HT * 1024) + lane * 16;
     auto dma = [&](int jh, int stage) {
-        _Float16* dst = lds + stage * HT_H + wv * 512;
-#pragma unroll
-        for (int i = 0; i < DMA_PER_HT; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc,
-                                                     (__attribute__((address_space(3))) void*)(dst + i * NTHR * 8),
-                                                     16, dma_off, (h0 + jh) * (HT_H * 2) + i * (NTHR * 16), 0, 0);
+        auto* dst = (__attribute__((address_space(3))) void*)(lds + stage * HT_H + wv * (DMA_PER_HT * 512));
+        const int so = (h0 + jh) * (HT_H * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 1024, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 2048, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 3072, 0);
     };
     // operand reads through 32-bit LDS byte addresses: base + immediate offsets fold into ds_read_b128
     auto kptr = [&](int stage) {

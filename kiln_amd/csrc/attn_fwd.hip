@@ -259,7 +259,7 @@ constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = 4;
 constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
 static_assert(DMA_PER_HT == 4, "a wave copies four 1 KB pieces of each half tile");
 constexpr int PART_FLOATS = BM * HD + 2 * BM;      // one key range's partial result of a query tile
-static_assert(NS >= 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration)");
+static_assert(NS == 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration); half tile j in stage j % 4");
 
 template <typename InT, typename OutT, bool QNORM, bool ROPE>
 __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 2nd: waves per SIMD
@@ -391,13 +391,12 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         return __builtin_amdgcn_ballot_w64(need) != 0;
     };
 
-    int st = 0;        // stage of half tile j
-    int st2 = NS - 1;  // stage that receives half tile j+NS-1
+    auto stage = [](int jh) { return jh & (NS - 1); };  // LDS stage of half tile jh
     // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
     auto step = [&](auto maskn_tag, int j, floatx4 (&cur)[2][2], floatx4 (&sn)[2][2]) {
         constexpr bool MASKN = decltype(maskn_tag)::value;
         if (need_rescale()) rescale(cur);  // lazy rescale (rare)
-        const int st1 = st == NS - 1 ? 0 : st + 1;
+        const int st = stage(j), st1 = stage(j + 1);
         half8 va[4];
         {
             const lds_half8* kp = kptr(st1);
@@ -435,11 +434,10 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         if constexpr (MASKN) KILN_WAIT_VMCNT(0);
         else KILN_WAIT_VMCNT((NS - 4) * DMA_PER_HT);
         __builtin_amdgcn_s_barrier();
-        dma(min(j + NS - 1, nh - 1), st2);  // into the stage of tile j-1
-        st2 = st2 == NS - 1 ? 0 : st2 + 1;
+        dma(min(j + NS - 1, nh - 1), stage(j + NS - 1));  // into the stage of tile j-1
         half8 vb[4];
         {
-            const lds_half8* kp = kptr(st1 == NS - 1 ? 0 : st1 + 1);  // K_{j+2}; past the end: stale, unused
+            const lds_half8* kp = kptr(stage(j + 2));  // K_{j+2}; past the end: stale, unused
 #pragma unroll
             for (int s = 0; s < 4; s++) ka[s] = kp[s * 64];
             const lds_half8* vp = kptr(st) + 32 * HD / 8 + 4 * 64;
@@ -460,7 +458,6 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
             for (int qb = 0; qb < 2; qb++) o[qb][db + 4] = mfma16(vb[db], pb[qb], o[qb][db + 4]);
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) mx[qb] = max8(sn[0][qb], sn[1][qb]);
-        st = st1;
         KILN_FENCE();
     };
 
@@ -496,7 +493,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
     if (need_rescale()) rescale(sc);
     {
         half8 va[8];
-        const lds_half8* vp = kptr(st) + 32 * HD / 8;
+        const lds_half8* vp = kptr(stage(j)) + 32 * HD / 8;
 #pragma unroll
         for (int db = 0; db < 8; db++) va[db] = vp[db * 64];
 #pragma unroll

@@ -41,6 +41,7 @@ struct AttnParams {
     int ksplit;   // key ranges per (query tile, head, job): > 1 writes partial (m, l, O) for k_attn_merge
     float* part;  // partials: [unit][ksplit] x (O [128 rows][128] fp32, then (m, l) per row)
     int store_pairs;  // ldo or an output base not 8/16-byte aligned: store element pairs
+    int store_rows;   // ldo and every output base 16-byte aligned: output rows staged through LDS
     const uint16_t* qw;
     float eps, qscale;
     const float* rcos;
@@ -229,6 +230,45 @@ __device__ __forceinline__ void epilogue(const AttnParams& p, const AttnJob& J, 
 #pragma unroll
     for (int db = 0; db < 8; db++)
         store4<OutT>(orow + 16 * db, o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv, pairs);
+}
+
+// The same through LDS, for aligned outputs: the wave's 16 normalized rows of one query block go row-major into
+// its LDS region (rows padded by 16 bytes: the 16 rows of a write land in different banks), then leave as whole
+// rows, 16 bytes per lane (a 256-byte fp16 row from 16 lanes, a 512-byte fp32 row from 32), instead of 8-byte
+// pieces of 16 rows per store instruction.
+template <typename OutT>
+constexpr int ORS = HD + 16 / (int)sizeof(OutT);  // LDS row stride of the staged output, elements
+template <typename OutT>
+__device__ __forceinline__ void epilogue_rows(const AttnParams& p, const AttnJob& J, int row0, int h, int g, int lane,
+                                              float m, float l, const floatx4 (&o)[8], OutT* stg) {
+    float lt = quad_sum(l);
+    float sc = 1.f;
+    if (J.npad) {
+        const float mn = fmaxf(m, 0.f);
+        sc = __builtin_amdgcn_exp2f(m - mn);
+        lt = lt * sc + (float)J.npad * __builtin_amdgcn_exp2f(-mn);
+    }
+    const float inv = sc / lt;
+    OutT* srow = stg + (lane & 15) * ORS<OutT> + 4 * g;
+#pragma unroll
+    for (int db = 0; db < 8; db++) {
+        if constexpr (std::is_same<OutT, _Float16>::value)
+            *reinterpret_cast<half4*>(srow + 16 * db) = half4{(_Float16)(o[db][0] * inv), (_Float16)(o[db][1] * inv),
+                                                              (_Float16)(o[db][2] * inv), (_Float16)(o[db][3] * inv)};
+        else
+            *reinterpret_cast<floatx4*>(srow + 16 * db) = o[db] * inv;
+    }
+    __builtin_amdgcn_wave_barrier();  // the wave's LDS writes precede its reads (one wave, in-order LDS queue)
+    constexpr int RPI = 64 * 16 / (HD * (int)sizeof(OutT));  // rows per 16-byte-per-lane instruction: 4 or 2
+    constexpr int LPR = 64 / RPI;                              // lanes per row
+#pragma unroll
+    for (int i = 0; i < 16 / RPI; i++) {
+        const int r = RPI * i + lane / LPR, col = (lane % LPR) * (16 / (int)sizeof(OutT));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * ORS<OutT> + col);
+        if (row0 + r < p.Tq)
+            *reinterpret_cast<u32x4*>(reinterpret_cast<OutT*>(J.o) + (size_t)(row0 + r) * p.ldo + h * HD + col) = v;
+    }
+    __builtin_amdgcn_wave_barrier();  // reads done before the next block's writes reuse the region
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14)
@@ -510,7 +550,15 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
             for (int db = 0; db < 8; db++) o[qb][db] = mfma16(va[db], pb, o[qb][db]);
         }
     }
-    KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is released
+    KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is reused or released
+    if (p.ksplit <= 1 && p.store_rows) {
+        __builtin_amdgcn_s_barrier();  // every wave is done with the ring: its LDS now stages the output rows
+        OutT* stg = reinterpret_cast<OutT*>(lds) + wv * 16 * ORS<OutT>;
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++)
+            epilogue_rows<OutT>(p, J, W.qt * BM + wv * 32 + 16 * qb, W.h, g, lane, m[qb], l[qb], o[qb], stg);
+        return;
+    }
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
         if (p.ksplit > 1) {  // partial result of this key range: unnormalized O, running max m, row sum l
@@ -782,6 +830,9 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
     bool pairs = (a.ldo * osz) % (4 * osz) != 0;
     for (int i = 0; i < a.njobs; i++) pairs |= ((uintptr_t)a.job[i].o % (4 * osz)) != 0;
     p.store_pairs = pairs;
+    bool rows = (a.ldo * osz) % 16 == 0;
+    for (int i = 0; i < a.njobs; i++) rows &= ((uintptr_t)a.job[i].o % 16) == 0;
+    p.store_rows = rows;
     p.qw = a.qw;
     p.eps = a.eps;
     p.qscale = a.q_prescaled ? 1.0f : LOG2E / sqrtf((float)HD);

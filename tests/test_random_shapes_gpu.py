@@ -143,3 +143,29 @@ def _run_case(c, idx):
         kiln_amd.attention16(out, qd, kd, vd, Tq, Tk, H, D, npad=npad)
     torch.cuda.synchronize()
     assert_close(out.float().cpu().numpy(), ref, f"case {idx} {c['route']}")
+
+
+# Output row stride / base alignment -> store path of the attention epilogue: 16-byte aligned rows are staged
+# through LDS and stored as whole rows; 8-byte aligned fp16 rows take 4-element stores; anything else element
+# pairs.
+ALIGN_CASES = [(torch.float16, 0, 0), (torch.float16, 4, 0), (torch.float16, 2, 6), (torch.float32, 0, 4),
+               (torch.float32, 2, 0), (torch.float32, 4, 2)]
+
+
+@pytest.mark.parametrize("odt,off,pad", ALIGN_CASES)
+def test_output_alignment_paths(gpu, odt, off, pad):
+    H, B, Tq, Tk = 3, 2, 300, 257
+    g = torch.Generator().manual_seed(31 + off + pad)
+    print(f"[random] output alignment {odt} off={off} pad={pad}", flush=True)
+    q, k, v = (torch.randn(B * T_, H * D, generator=g).half().float() for T_ in (Tq, Tk, Tk))
+    qd = _strided(B * Tq, H, 8, 0, torch.float16, q)
+    kd = _strided(B * Tk, H, 0, 0, torch.float16, k)
+    vd = _strided(B * Tk, H, 24, 0, torch.float16, v)
+    out = _strided(B * Tq, H, pad, off, odt, None)
+    kiln_amd.attn_f16in(out, qd, kd, vd, B, Tq, Tk, H)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    for b in range(B):
+        ref = oracle.attn_f64(q[b * Tq:(b + 1) * Tq].numpy(), k[b * Tk:(b + 1) * Tk].numpy(),
+                              v[b * Tk:(b + 1) * Tk].numpy(), H)
+        assert_close(o[b * Tq:(b + 1) * Tq], ref, f"alignment {odt} off={off} pad={pad} b={b}")

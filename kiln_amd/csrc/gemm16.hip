@@ -198,6 +198,47 @@ __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)
             }
         }
     }
+    if (region == 2 && p.T % 32 == 0) {
+        // V through LDS, one head (128 columns) per pass: the wave pairs of that head write their fp16 values
+        // row-major (rows padded to 288 bytes), then every wave assembles whole 16-byte V^T operand units (8 keys of
+        // one d) with transposing reads, as the K/V prepare pass does, instead of 2-byte scatters. With T a
+        // multiple of 32 (and the tile's first row one too) no 32-key half tile straddles two items.
+        constexpr int VRS = HD + 16, BM = 32 * MB;
+        static_assert(BM * VRS <= GNS * Tile<MB>::STAGE_H, "the staged V tile fits in the ring's LDS");
+        const int i = lane & 15, gq = lane >> 4;
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        typedef short s8 __attribute__((ext_vector_type(8)));
+        typedef __attribute__((address_space(3))) s4 lds_s4;
+#pragma unroll
+        for (int pass = 0; pass < 2; pass++) {
+            if ((wn >> 1) == pass) {
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                    for (int nb = 0; nb < NBW; nb++) {
+                        const floatx4 v = acc[nb][mb];
+                        *reinterpret_cast<half4*>(lds + (wm * 16 * MB + mb * 16 + rl) * VRS + half * 64 + nb * 16 + cq) =
+                            half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                    }
+            }
+            __syncthreads();
+            const int hdp = (c0 + pass * HD) / HD;
+            for (int op = wv; op < (BM / 32) * 8; op += WAVES_N * WAVES_M) {
+                const int ht = op >> 3, db = op & 7, row0 = m0 + ht * 32;
+                if (row0 >= p.M) break;  // ops ascend with ht: every later one is past the matrix too
+                const int b = row0 / p.T, key0 = row0 - b * p.T;
+                const _Float16* src = lds + (ht * 32 + 4 * gq + (i >> 2)) * VRS + 16 * db + 4 * (i & 3);
+                const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)src);
+                const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(src + 16 * VRS));
+                _Float16* kv = reinterpret_cast<_Float16*>(p.kvp[b]) + (size_t)hdp * kv_head_stride(p.T) +
+                               (size_t)(key0 / KT) * KV_TILE_H;
+                *reinterpret_cast<s8*>(kv + kv_v_off((key0 % KT) / 32, db, lane)) =
+                    s8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+            __syncthreads();  // every read of this head's values precedes the next pass's writes
+        }
+        return;
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const int row = rbase + mb * 16;

@@ -46,6 +46,38 @@ __global__ __launch_bounds__(256) void k_matvec_bf16(float* __restrict__ y, cons
     if (lane == 0) y[row] = s + (add ? add[row - grp * grows] : 0.f);
 }
 
+// cols == 256 (the adaLN second layers): a row is 512 bytes, so a wave takes 8 rows, 4 per half wave, every load of
+// the 4 rows in flight together (one row per wave would leave half the lanes idle and one load per lane in flight)
+__global__ __launch_bounds__(256) void k_matvec_bf16_256(float* __restrict__ y, const uint16_t* __restrict__ W,
+                                                         const float* __restrict__ x, const float* __restrict__ add,
+                                                         int rows, int grows, int xstride) {
+    const int lane = threadIdx.x & 63, half = lane >> 5, l32 = lane & 31;
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + half * 4;
+    u32x4 raw[4];
+    floatx4 xa[4], xb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = min(r0 + i, rows - 1);
+        const float* xr = x + (size_t)(row / grows) * xstride + l32 * 8;
+        raw[i] = *reinterpret_cast<const u32x4*>(W + (size_t)row * 256 + l32 * 8);
+        xa[i] = *reinterpret_cast<const floatx4*>(xr);
+        xb[i] = *reinterpret_cast<const floatx4*>(xr + 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            s += __uint_as_float(raw[i][e] << 16) * (e < 2 ? xa[i][2 * e] : xb[i][2 * e - 4]);
+            s += __uint_as_float(raw[i][e] & 0xffff0000u) * (e < 2 ? xa[i][2 * e + 1] : xb[i][2 * e - 3]);
+        }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        const int row = r0 + i;
+        if (l32 == 0 && row < rows) y[row] = s + (add ? add[row % grows] : 0.f);
+    }
+}
+
 __global__ void k_silu(float* __restrict__ y, const float* __restrict__ x, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {
@@ -326,6 +358,12 @@ static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
 hipError_t launch_matvec_bf16(float* y, const uint16_t* W, const float* x, const float* add, int rows, int cols,
                               int groups, hipStream_t s) {
     const int grows = rows, xstride = groups > 1 ? cols : 0;
+    if (cols == 256 && ((size_t)W & 15) == 0 && ((size_t)x & 15) == 0) {
+        const int total = rows * groups;
+        hipLaunchKernelGGL(k_matvec_bf16_256, dim3((total + 31) / 32), dim3(256), 0, s, y, W, x, add, total, grows,
+                           xstride);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_matvec_bf16, dim3((rows * groups + 3) / 4), dim3(256), 0, s, y, W, x, add, rows * groups,
                        cols, grows, xstride);
     return hipGetLastError();

@@ -122,23 +122,34 @@ __device__ __forceinline__ float gelu_erf(float v) {
 }
 
 // EPI_QKV epilogue. The workgroup's 256 columns are two heads of one region (Q, K or V: D is a multiple of 256).
-// A wave holds 64 columns = half a head; its partner wave (wv ^ 2, the same rows) holds the other half. Q/K:
-// per-row sum of squares over the head (own half + partner's, through LDS), scale by rsqrt(mean + eps) and the
-// bf16 weight, then RoPE, whose pairs (i, i + 64) are the same accumulator element of the two partner waves
-// (exchanged through LDS two row blocks at a time). Q is stored as fp16(q * qscale) rows, K and V in the
-// prepared K/V layout of their item (kv_k_el / kv_v_el).
+// A wave holds 64 columns = half a head; its partner wave (wv ^ 2, the same rows) holds the other half. In the Q and
+// K regions the k loop read the wave's W blocks so that block nb holds head dims dq(nb) + 0..15, dq(nb) =
+// 32*(wn & 1) + 16*(nb & 1) + 64*(nb >> 1): each RoPE pair (i, i + 64) is element (nb, e) and (nb + 2, e) of one
+// lane. Q/K: per-row sum of squares over the head (own half + partner's, through LDS), scale by rsqrt(mean + eps)
+// and the bf16 weight, then RoPE in registers. Q is stored as fp16(q * qscale) rows, K and V in the prepared K/V
+// layout of their item (kv_k_el / kv_v_el).
 template <int MB>
 __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)[NBW][MB], _Float16* lds, int m0,
                                              int n0, int wv, int wn, int wm, int lane) {
     const int D = p.H * HD;
     const int region = n0 / D, c0 = n0 - region * D;
-    const int hd = (c0 + wn * 64) / HD, half = wn & 1;
-    const int rl = lane & 15, cq = 4 * (lane >> 4);  // column within the wave's 64: nb*16 + cq + e
+    const int hd = (c0 + (wn >> 1) * HD) / HD, half = wn & 1;
+    const int rl = lane & 15, cq = 4 * (lane >> 4);  // column within a 16-column block: cq + e
     const int rbase = m0 + wm * 16 * MB + rl;
+    auto dq = [&](int nb) { return 32 * half + 16 * (nb & 1) + 64 * (nb >> 1); };  // Q/K head dim of block nb
     float* lf = reinterpret_cast<float*>(lds);
     __syncthreads();  // every wave is done with the k loop's LDS stages
     if (region < 2) {
         const uint16_t* w = region == 0 ? p.qw : p.kw;
+        float wt[NBW][4];
+#pragma unroll
+        for (int nb = 0; nb < NBW; nb++) {
+            const uint2 wr = *reinterpret_cast<const uint2*>(w + dq(nb) + cq);  // 4 bf16
+            wt[nb][0] = __uint_as_float(wr.x << 16);
+            wt[nb][1] = __uint_as_float(wr.x & 0xffff0000u);
+            wt[nb][2] = __uint_as_float(wr.y << 16);
+            wt[nb][3] = __uint_as_float(wr.y & 0xffff0000u);
+        }
         float r[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
@@ -155,44 +166,26 @@ __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)
         __syncthreads();
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) r[mb] = rsqrtf((r[mb] + lf[(wv ^ 2) * 16 * MB + mb * 16 + rl]) * (1.0f / HD) + p.eps);
-        float wt[NBW][4];
-#pragma unroll
-        for (int nb = 0; nb < NBW; nb++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) wt[nb][e] = bf16_to_f32(w[half * 64 + nb * 16 + cq + e]);
 #pragma unroll
         for (int mb = 0; mb < MB; mb++)
 #pragma unroll
             for (int nb = 0; nb < NBW; nb++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[nb][mb][e] *= r[mb] * wt[nb][e];
-        // RoPE partner exchange, two row blocks per round: [wave][mb in round][nb][lane][e] (no tables: no RoPE,
-        // the cross-attention Q projection)
-        constexpr int XW = 2 * NBW * 64 * 4;  // floats per wave per round
+        if (p.rcos) {  // RoPE (none for the cross-attention Q projection)
 #pragma unroll
-        for (int g0 = 0; g0 < (p.rcos ? MB : 0); g0 += 2) {
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                if (g0 + j < MB)
-#pragma unroll
-                    for (int nb = 0; nb < NBW; nb++)
-                        *reinterpret_cast<floatx4*>(lf + wv * XW + ((j * NBW + nb) * 64 + lane) * 4) = acc[nb][g0 + j];
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                if (g0 + j >= MB) continue;
-                const int row = rbase + (g0 + j) * 16;
+            for (int mb = 0; mb < MB; mb++) {
+                const int row = rbase + mb * 16;
                 const int t = (row < p.M ? row : 0) % p.T;
 #pragma unroll
-                for (int nb = 0; nb < NBW; nb++) {
-                    const floatx4 o = *reinterpret_cast<const floatx4*>(lf + (wv ^ 2) * XW + ((j * NBW + nb) * 64 + lane) * 4);
-                    const floatx4 cs = *reinterpret_cast<const floatx4*>(p.rcos + (size_t)t * 64 + nb * 16 + cq);
-                    const floatx4 sn = *reinterpret_cast<const floatx4*>(p.rsin + (size_t)t * 64 + nb * 16 + cq);
+                for (int nb = 0; nb < 2; nb++) {
+                    const floatx4 cs = *reinterpret_cast<const floatx4*>(p.rcos + (size_t)t * 64 + dq(nb) + cq);
+                    const floatx4 sn = *reinterpret_cast<const floatx4*>(p.rsin + (size_t)t * 64 + dq(nb) + cq);
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        const float v = acc[nb][g0 + j][e];
-                        acc[nb][g0 + j][e] = half == 0 ? v * cs[e] - o[e] * sn[e] : v * cs[e] + o[e] * sn[e];
+                        const float a = acc[nb][mb][e], b = acc[nb + 2][mb][e];
+                        acc[nb][mb][e] = a * cs[e] - b * sn[e];
+                        acc[nb + 2][mb][e] = b * cs[e] + a * sn[e];
                     }
                 }
             }
@@ -249,7 +242,8 @@ __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)
         const int kc = (key % KT) / 32, k32 = key % 32;
 #pragma unroll
         for (int nb = 0; nb < NBW; nb++) {
-            const int d = half * 64 + nb * 16 + cq;  // 4 consecutive d, inside one 8-element chunk
+            // 4 consecutive d, inside one 8-element chunk (Q/K: the permuted head dims; V: the plain ones)
+            const int d = (region < 2 ? dq(nb) : half * 64 + nb * 16) + cq;
             const floatx4 v = acc[nb][mb];
             if (region == 0) {
                 *reinterpret_cast<half4*>(p.q16 + (size_t)row * D + hd * HD + d) =
@@ -357,10 +351,14 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
     const uint32_t lds_base = (uint32_t)(size_t)(__attribute__((address_space(3))) _Float16*)lds;
     const int rl = lane & 15;
     const uint32_t swz = (uint32_t)((((lane >> 4) ^ ((rl >> 1) & 3))) * 16);
-    const uint32_t wbase = lds_base + (uint32_t)((wn * NBW * 16 + rl) * 64) + swz;
+    // EPI_QKV, Q and K regions: the wave's W blocks are the head rows 32*(wn & 1) + {0, 16, 64, 80} instead of
+    // 64*(wn & 1) + {0, 16, 32, 48}, so that each RoPE pair (d, d + 64) lands in one lane (blocks nb and nb + 2)
+    const bool qkperm = EPI == EPI_QKV && n0 / (p.H * HD) < 2;
+    const uint32_t wbase = lds_base + (uint32_t)((((wn >> 1) * 128 + (wn & 1) * (qkperm ? 32 : 64)) + rl) * 64) + swz;
+    const uint32_t wbase_hi = wbase + (qkperm ? 2048u : 0u);  // blocks nb >= 2
     const uint32_t abase = lds_base + (uint32_t)(W_REG_H * 2 + (wm * MB * 16 + rl) * 64) + swz;
     auto wfrag = [&](int stage, int nb) {
-        return reinterpret_cast<const lds_half8*>((size_t)(wbase + stage * STAGE_H * 2))[nb * 64];
+        return reinterpret_cast<const lds_half8*>((size_t)((nb < 2 ? wbase : wbase_hi) + stage * STAGE_H * 2))[nb * 64];
     };
     auto afrag = [&](int stage, int mb) {
         return reinterpret_cast<const lds_half8*>((size_t)(abase + stage * STAGE_H * 2))[mb * 64];

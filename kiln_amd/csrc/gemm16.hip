@@ -143,13 +143,9 @@ __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)
         const uint16_t* w = region == 0 ? p.qw : p.kw;
         float wt[NBW][4];
 #pragma unroll
-        for (int nb = 0; nb < NBW; nb++) {
-            const uint2 wr = *reinterpret_cast<const uint2*>(w + dq(nb) + cq);  // 4 bf16
-            wt[nb][0] = __uint_as_float(wr.x << 16);
-            wt[nb][1] = __uint_as_float(wr.x & 0xffff0000u);
-            wt[nb][2] = __uint_as_float(wr.y << 16);
-            wt[nb][3] = __uint_as_float(wr.y & 0xffff0000u);
-        }
+        for (int nb = 0; nb < NBW; nb++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) wt[nb][e] = bf16_to_f32(w[dq(nb) + cq + e]);  // any alignment of w
         float r[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {

@@ -372,9 +372,176 @@ __global__ __launch_bounds__(256) void k_exact_attn(float* out, int ldo, const f
     if (tid < Dh) out[(size_t)t * ldo + (size_t)h * Dh + tid] = acc / l;
 }
 
+// ---- the same for Dh = 128 on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 products and sums, as the
+// reference's cuBLAS SGEMM fallback computes them) with an online softmax over 32-key tiles ----
+// Workgroup = 4 waves x 32 query rows of one head. Per 16-key block a wave computes S^T = K Q^T for its two 16-row
+// query blocks (32 MFMAs each, over d = 32g + s in lane group g and step s) and O^T += V^T P^T (8 d blocks x 4
+// steps): P^T comes straight out of the S^T accumulators (lane group g holds keys 4g + i, i = 0..3, of query
+// lane & 15; step kk takes element kk, and the V^T operand of lane (g, dd) is row 4g + kk of the block at
+// d = 8 dd + db, so the output accumulator db holds d = 32g + 8i + db). K/V tiles are staged in LDS as fp32 with
+// 132-float rows (conflict-free operand reads), two stages.
+constexpr int X_KT = 32, X_RS = 132, X_BM = 128;
+constexpr int X_STAGE = 2 * X_KT * X_RS;  // floats: K then V
+
+__global__ __launch_bounds__(256, 2) void k_exact_attn128(float* out, int ldo, const float* q, int ldq,
+                                                          const float* k, int ldk, const float* v, int ldv, int Tq,
+                                                          int Tk, int causal, int npad, float scale) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // 2 stages
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const int h = blockIdx.y, q0 = blockIdx.x * X_BM + wv * 32;
+    // Q operands: query block qb, row q0 + 16 qb + n, d = 32 g .. 32 g + 31 (rows past Tq read row Tq - 1)
+    float qo[2][32];
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const float* qr = q + (size_t)min(q0 + 16 * qb + n, Tq - 1) * ldq + (size_t)h * 128 + 32 * g;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const floatx4 t = *reinterpret_cast<const floatx4*>(qr + 4 * c);
+#pragma unroll
+            for (int e = 0; e < 4; e++) qo[qb][4 * c + e] = t[e];
+        }
+    }
+    // the tile loads of this thread: row tid / 8 of the tile, floats 16 (tid % 8) .. + 16, of K and of V
+    const int lr = tid >> 3, lc = (tid & 7) * 16;
+    floatx4 kr[4], vr[4];
+    auto load = [&](int t) {  // keys past Tk read the last key and are zeroed (no divergent branch)
+        const int key = t * X_KT + lr;
+        const bool in = key < Tk;
+        const float* kp = k + (size_t)min(key, Tk - 1) * ldk + (size_t)h * 128 + lc;
+        const float* vp = v + (size_t)min(key, Tk - 1) * ldv + (size_t)h * 128 + lc;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const floatx4 a = *reinterpret_cast<const floatx4*>(kp + 4 * c);
+            const floatx4 b = *reinterpret_cast<const floatx4*>(vp + 4 * c);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                kr[c][e] = in ? a[e] : 0.f;
+                vr[c][e] = in ? b[e] : 0.f;
+            }
+        }
+    };
+    auto store = [&](int st) {
+        float* ks = xs + st * X_STAGE;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            *reinterpret_cast<floatx4*>(ks + lr * X_RS + lc + 4 * c) = kr[c];
+            *reinterpret_cast<floatx4*>(ks + X_KT * X_RS + lr * X_RS + lc + 4 * c) = vr[c];
+        }
+    };
+    // causal: no key past the last query row of the workgroup
+    const int kend = causal ? min(Tk, blockIdx.x * X_BM + X_BM) : Tk;
+    const int nt = (kend + X_KT - 1) / X_KT;
+    floatx4 o[2][8];
+    float m[2], l[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+#pragma unroll
+        for (int db = 0; db < 8; db++) o[qb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+        m[qb] = npad ? 0.f : -INFINITY;  // with padding keys the max starts at their score, 0
+        l[qb] = 0.f;
+    }
+    if (nt > 0) {
+        load(0);
+        store(0);
+        if (nt > 1) load(1);
+    }
+    for (int t = 0; t < nt; t++) {
+        __syncthreads();  // tile t stored by every thread
+        const float* ks = xs + (t & 1) * X_STAGE;
+        const float* vs = ks + X_KT * X_RS;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            floatx4 sc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+            const float* krow = ks + (kb * 16 + n) * X_RS + 32 * g;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const floatx4 ka = *reinterpret_cast<const floatx4*>(krow + 4 * c);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int qb = 0; qb < 2; qb++)
+                        sc[qb] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[e], qo[qb][4 * c + e], sc[qb], 0, 0, 0);
+            }
+            float pr[2][4];
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                const int row = q0 + 16 * qb + n;
+                float bm = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int key = t * X_KT + kb * 16 + 4 * g + i;
+                    const bool in = key < Tk && (!causal || key <= row);
+                    sc[qb][i] = in ? sc[qb][i] * scale : -INFINITY;
+                    bm = fmaxf(bm, sc[qb][i]);
+                }
+                bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+                bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+                const float mn = fmaxf(m[qb], bm);
+                const float corr = mn == -INFINITY ? 1.f : expf(m[qb] - mn);
+                m[qb] = mn;
+                l[qb] *= corr;
+#pragma unroll
+                for (int db = 0; db < 8; db++) o[qb][db] *= corr;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    pr[qb][i] = sc[qb][i] == -INFINITY ? 0.f : expf(sc[qb][i] - mn);
+                    l[qb] += pr[qb][i];
+                }
+            }
+            // O^T += V^T P^T: step kk takes key 4g + kk of the block in lane group g
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const float* vrow = vs + (kb * 16 + 4 * g + kk) * X_RS + 8 * n;
+                const floatx4 va = *reinterpret_cast<const floatx4*>(vrow);
+                const floatx4 vb = *reinterpret_cast<const floatx4*>(vrow + 4);
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+                    for (int db = 0; db < 8; db++)
+                        o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(db < 4 ? va[db] : vb[db - 4], pr[qb][kk],
+                                                                         o[qb][db], 0, 0, 0);
+            }
+        }
+        if (t + 1 < nt) {
+            store((t + 1) & 1);  // its stage's tile t-1 was read before this iteration's barrier
+            if (t + 2 < nt) load(t + 2);
+        }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        float lt = l[qb] + __shfl_xor(l[qb], 16, 64);
+        lt += __shfl_xor(lt, 32, 64);
+        if (npad) lt += (float)npad * expf(-m[qb]);
+        const float inv = 1.f / lt;
+        const int row = q0 + 16 * qb + n;
+        if (row >= Tq) continue;
+        float* orow = out + (size_t)row * ldo + (size_t)h * 128 + 32 * g;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            floatx4 a, b;
+#pragma unroll
+            for (int db = 0; db < 4; db++) {
+                a[db] = o[qb][db][i] * inv;
+                b[db] = o[qb][db + 4][i] * inv;
+            }
+            *reinterpret_cast<floatx4*>(orow + 8 * i) = a;
+            *reinterpret_cast<floatx4*>(orow + 8 * i + 4) = b;
+        }
+    }
+}
+
 hipError_t launch_exact_attn(float* out, int ldo, const float* q, int ldq, const float* k, int ldk, const float* v,
                              int ldv, int Tq, int Tk, int H, int Dh, bool causal, int npad, hipStream_t s) {
     if (Tq <= 0 || H <= 0) return hipSuccess;
+    const auto a16 = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+    if (Dh == 128 && Tk > 0 && a16(q) && a16(k) && a16(v) && a16(out) && ldq % 4 == 0 && ldk % 4 == 0 &&
+        ldv % 4 == 0 && ldo % 4 == 0) {
+        hipLaunchKernelGGL(k_exact_attn128, dim3((Tq + X_BM - 1) / X_BM, H), dim3(256),
+                           (size_t)2 * X_STAGE * sizeof(float), s, out, ldo, q, ldq, k, ldk, v, ldv, Tq, Tk,
+                           causal ? 1 : 0, npad, 1.f / sqrtf(128.f));
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_exact_attn, dim3(Tq, H), dim3(256), 0, s, out, ldo, q, ldq, k, ldk, v, ldv, Tk, Dh,
                        causal ? 1 : 0, npad, 1.f / sqrtf((float)Dh));
     return hipGetLastError();

@@ -276,6 +276,31 @@ def test_exact_attention(gpu, Dh, causal, npad):
     assert_close(out.cpu().numpy(), ref, f"exact Dh={Dh} causal={causal}", max_abs=1e-5, mean_abs=1e-6)
 
 
+@pytest.mark.parametrize("Tq,Tk,Hh,causal,npad,pad", [(1000, 777, 3, False, 5, 64), (300, 300, 2, True, 0, 0),
+                                                       (129, 40, 1, True, 3, 4), (33, 1, 2, False, 0, 0)])
+def test_exact_attention_dh128_mfma(gpu, Tq, Tk, Hh, causal, npad, pad):
+    """kiln_attn_fwd_exact at Dh = 128 (the fp32 matrix-core kernel): ragged query and key counts, causal with
+    Tq != Tk, padding keys, and rows padded beyond H*128 (the head block at a column offset inside the row), against
+    the float64 oracle at the exact path's bar."""
+    D_ = 128
+    q = randn(61, Tq, Hh * D_)
+    k = randn(62, Tk, Hh * D_)
+    v = randn(63, Tk, Hh * D_)
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), Hh, Dh=D_, npad=npad, causal=causal)
+
+    def padded(t):
+        buf = torch.zeros(t.shape[0], t.shape[1] + pad, device=DEV)
+        buf[:, pad // 2:pad // 2 + t.shape[1]] = t.to(DEV)
+        return buf[:, pad // 2:pad // 2 + t.shape[1]]
+    out_full = torch.full((Tq, Hh * D_ + pad), float("nan"), device=DEV)
+    out = out_full[:, pad // 2:pad // 2 + Hh * D_]
+    kiln_amd.attention_exact(out, padded(q), padded(k), padded(v), Tq, Tk, Hh, D_, causal=causal, npad=npad)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, f"exact Dh=128 Tq={Tq} Tk={Tk}", max_abs=1e-5, mean_abs=1e-6)
+    if pad:  # the padding columns of the output rows are untouched
+        assert torch.isnan(out_full[:, :pad // 2]).all() and torch.isnan(out_full[:, pad // 2 + Hh * D_:]).all()
+
+
 # ---- the bandwidth-bound ops around attention ----
 def test_rmsnorm_rope_nag_kernels(gpu):
     T = 96

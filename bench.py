@@ -461,6 +461,17 @@ def main():
     cfgb_flop = cfgb["flop"]
     ms_s8 = tm.run(cfgb["sample8"], 2, 1)
     log(f"config 5, 8-step Euler sampling with CFG 4.5 + NAG (8 forwards of the CFG pair): {ms_s8:.1f} ms")
+    # the fp32 branch of the same forward (the reference's "precision": "fp32" jobs: fp32 linears, RMSNorm, RoPE,
+    # exact fp32 attention), contexts cached for it
+    from kiln_amd import dit as _dit
+    g32 = torch.Generator(device=dev).manual_seed(32)
+    cs32 = [cfgb["dit"].cache_context(torch.randn(512, 1024, generator=g32, device=dev), fp32=True) for _ in range(3)]
+    lat32 = torch.randn(16, 96, 144, generator=g32, device=dev)
+    outs32 = [torch.empty_like(lat32) for _ in range(2)]
+    nag32 = _dit.Nag(cs32[2], 5.0, 2.5, 0.25)
+    ms_f32 = tm.run(lambda: cfgb["dit"].forward(outs32, lat32, 0.5, cs32[:2], nag=nag32, fp32=True), 2, 1)
+    log(f"config 5, DiT forward of the CFG pair on the fp32 path: {ms_f32:.1f} ms per step")
+    del cs32, outs32, nag32
     del cfgb
 
     # HBM bytes per launch of k_attn_fwd (config 4): the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs, with the
@@ -521,6 +532,7 @@ def main():
             "dit_forward_ms_per_step": round(ms_blk, 3),
             "dit_forward_tflops": round(cfgb_flop / ms_blk / 1e9, 1),
             "dit_sample_8_steps_ms": round(ms_s8, 1),
+            "dit_forward_fp32_path_ms_per_step": round(ms_f32, 1),
             "dit_forward_workload": "config 5: Dit::forward_batch of the CFG pair on the fp16 path (step tables, patch "
                                     "embed, 28 x (3 LN16 + Q/K/V, O, cross-Q, cross-O, MLP linear16 + self-attn + "
                                     "cross-attn L=512 + NAG), final layer), B=2, T=3456, 2B shapes",

@@ -382,8 +382,115 @@ hipError_t launch_unpatchify(float* lat, const float* tok, int ldt, int Hl, int 
     hipLaunchKernelGGL(k_unpatchify, dim3(nblk(n)), dim3(256), 0, s, lat, tok, ldt, Hl, Wl);
     return hipGetLastError();
 }
+// The same product for the DiT's large fp32 linears (K a multiple of 32, 16-byte aligned rows): workgroup tile 64
+// rows x 128 output columns, k chunks of 32 staged in LDS (x as fp32, W as bf16, rows padded so the 16 rows of an
+// operand read land in distinct banks), two stages, the next chunk's global loads in registers during the current
+// chunk's MFMAs; 4 waves as 2 x 2, each 32 rows x 64 columns (2 x 4 blocks of v_mfma_f32_16x16x4_f32), the k
+// mapping of k_linear_f32 (lane group g holds k 8g .. 8g + 8 of the chunk, step s takes element s).
+constexpr int LF_BM = 64, LF_BN = 128, LF_BK = 32;
+constexpr int LF_XS = 36;  // x row stride in LDS, floats (144 bytes)
+constexpr int LF_WS = 40;  // W row stride in LDS, bf16 (80 bytes)
+constexpr int LF_XB = LF_BM * LF_XS * 4, LF_STAGE = LF_XB + LF_BN * LF_WS * 2;
+
+__global__ __launch_bounds__(256, 2) void k_linear_f32t(float* __restrict__ y, int ldy, const float* __restrict__ x,
+                                                        int ldx, const uint16_t* __restrict__ W, int T, int rows,
+                                                        int cols) {
+    __shared__ __attribute__((aligned(16))) unsigned char sm[2 * LF_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wr = wv >> 1, wc = wv & 1, i = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.x * LF_BM, n0 = blockIdx.y * LF_BN;
+    // this thread's global pieces of a chunk: x rows f / 8 (f = tid + 256 r), 4 floats at 4 (f % 8); W rows f / 4,
+    // 8 bf16 at 8 (f % 4); rows past the matrix read its last row (results unused)
+    const float* xp[2];
+    const uint16_t* wp[2];
+    uint32_t xo_l[2], wo_l[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int f = tid + 256 * r;
+        xp[r] = x + (size_t)min(m0 + f / 8, T - 1) * ldx + 4 * (f % 8);
+        xo_l[r] = (uint32_t)(((f / 8) * LF_XS + 4 * (f % 8)) * 4);
+        wp[r] = W + (size_t)min(n0 + f / 4, rows - 1) * cols + 8 * (f % 4);
+        wo_l[r] = (uint32_t)(LF_XB + ((f / 4) * LF_WS + 8 * (f % 4)) * 2);
+    }
+    floatx4 xr[2];
+    u32x4 wr4[2];
+    auto load = [&](int kc) {
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            xr[r] = *reinterpret_cast<const floatx4*>(xp[r] + kc * LF_BK);
+            wr4[r] = *reinterpret_cast<const u32x4*>(wp[r] + kc * LF_BK);
+        }
+    };
+    auto store = [&](int st) {
+        unsigned char* b = sm + st * LF_STAGE;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            *reinterpret_cast<floatx4*>(b + xo_l[r]) = xr[r];
+            *reinterpret_cast<u32x4*>(b + wo_l[r]) = wr4[r];
+        }
+    };
+    floatx4 acc[2][4] = {};
+    const int nk = cols / LF_BK;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; kc++) {
+        if (kc + 1 < nk) load(kc + 1);
+        const unsigned char* b = sm + (kc & 1) * LF_STAGE;
+        float xo[2][8], wo[4][8];
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+            const float* xs = reinterpret_cast<const float*>(b) + (32 * wr + 16 * rb + i) * LF_XS + 8 * g;
+            const floatx4 a = *reinterpret_cast<const floatx4*>(xs), c = *reinterpret_cast<const floatx4*>(xs + 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                xo[rb][e] = a[e];
+                xo[rb][e + 4] = c[e];
+            }
+        }
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                reinterpret_cast<const uint16_t*>(b + LF_XB) + (64 * wc + 16 * cb + i) * LF_WS + 8 * g);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                wo[cb][2 * e] = __uint_as_float(raw[e] << 16);
+                wo[cb][2 * e + 1] = __uint_as_float(raw[e] & 0xffff0000u);
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 4; cb++)
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xo[rb][st], wo[cb][st], acc[rb][cb], 0, 0, 0);
+        if (kc + 1 < nk) store((kc + 1) & 1);  // its stage's chunk kc-1 was read before the last barrier
+        __syncthreads();
+    }
+    // lane holds column n0 + 64 wc + 16 cb + i of rows m0 + 32 wr + 16 rb + 4 g + r
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++) {
+        const int n = n0 + 64 * wc + 16 * cb + i;
+        if (n >= rows) continue;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = m0 + 32 * wr + 16 * rb + 4 * g + r;
+                if (t < T) y[(size_t)t * ldy + n] = acc[rb][cb][r];
+            }
+    }
+}
+
 hipError_t launch_linear_f32(float* y, int ldy, const float* x, int ldx, const uint16_t* W, int T, int rows, int cols,
                              hipStream_t s) {
+    if (cols % LF_BK == 0 && ldx % 4 == 0 && ((size_t)x & 15) == 0 && ((size_t)W & 15) == 0 && T >= LF_BM &&
+        rows >= LF_BN) {
+        hipLaunchKernelGGL(k_linear_f32t, dim3((T + LF_BM - 1) / LF_BM, (rows + LF_BN - 1) / LF_BN), dim3(256), 0, s,
+                           y, ldy, x, ldx, W, T, rows, cols);
+        return hipGetLastError();
+    }
     const long waves = (long)((T + 15) / 16) * ((rows + 63) / 64);
     hipLaunchKernelGGL(k_linear_f32, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, y, ldy, x, ldx, W, T, rows,
                        cols);

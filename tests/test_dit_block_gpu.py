@@ -244,7 +244,8 @@ def test_linear_f32_patchify_silu_cfg(gpu):
     out = torch.full((16, Hl, Wl), float("nan"), device=DEV)
     kiln_amd.unpatchify(out, y.to(DEV)[:, :64])
     np.testing.assert_array_equal(out.cpu().numpy(), oracle.unpatchify(y[:, :64].contiguous().numpy(), Hl, Wl))
-    for T_, rows, cols in [(77, 2048, 68), (300, 64, 2048)]:
+    # (77, 2048, 68) and (300, 64, 2048) take the one-wave kernel; the others the LDS-tiled one (ragged T and rows)
+    for T_, rows, cols in [(77, 2048, 68), (300, 64, 2048), (300, 200, 96), (513, 384, 512)]:
         x = torch.randn(T_, cols, generator=g)
         W = _bf16w(g, rows, cols)
         yy = torch.empty(T_, rows, device=DEV)

@@ -375,7 +375,12 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         for (int db = 0; db < 8; db++) o[qb][db] = floatx4{0.f, 0.f, 0.f, 0.f};
         l[qb] = 0.f;
     }
-    const half2v ones = {(_Float16)1.f, (_Float16)1.f};
+    // Row sums on the matrix core: P^T times a 9th V^T block of ones (constant registers, no LDS read), whose
+    // accumulator holds the row's sum of the fp16-rounded P values the PV MFMAs consume in every one of its rows:
+    // two MFMAs per half tile instead of eight v_dot2c_f32_f16 on the VALU, which bounds the loop.
+    const half8 ones8 = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
+                         (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+    floatx4 lsum[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 
     half8 ka[8];  // K operands s = 2c + kb: d chunks 0-1 (s < 4) of the next QK chains are read a phase ahead
 #pragma unroll
@@ -416,7 +421,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
             const float corr = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
             for (int db = 0; db < 8; db++) o[qb][db] *= corr;
-            l[qb] *= corr;
+            lsum[qb] *= corr;
             m[qb] += d;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -462,9 +467,6 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
             const int qb = s >> 2, e = (2 * s) % 8, kb = e / 4, i = e % 4;
             pb[qb][e] = (_Float16)__builtin_amdgcn_exp2f(cur[kb][qb][i]);
             pb[qb][e + 1] = (_Float16)__builtin_amdgcn_exp2f(cur[kb][qb][i + 1]);
-            // row sum of the fp16-rounded P values the PV MFMA consumes
-            const half2v pr = {pb[qb][e], pb[qb][e + 1]};
-            l[qb] = __builtin_amdgcn_fdot2(pr, ones, l[qb], false);
         }
         KILN_FENCE();
 
@@ -496,6 +498,8 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         for (int db = 0; db < 4; db++)
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) o[qb][db + 4] = mfma16(vb[db], pb[qb], o[qb][db + 4]);
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) lsum[qb] = mfma16(ones8, pb[qb], lsum[qb]);
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) mx[qb] = max8(sn[0][qb], sn[1][qb]);
         KILN_FENCE();
@@ -541,15 +545,14 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
             half8 pb;
 #pragma unroll
             for (int e = 0; e < 8; e++) pb[e] = (_Float16)__builtin_amdgcn_exp2f(sc[e / 4][qb][e % 4]);
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const half2v pr = {pb[e], pb[e + 1]};
-                l[qb] = __builtin_amdgcn_fdot2(pr, ones, l[qb], false);
-            }
+            lsum[qb] = mfma16(ones8, pb, lsum[qb]);
 #pragma unroll
             for (int db = 0; db < 8; db++) o[qb][db] = mfma16(va[db], pb, o[qb][db]);
         }
     }
+    // every row of the ones block holds the full sum: a quarter in each of the four lanes the epilogue adds (exact)
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) l[qb] = lsum[qb][0] * 0.25f;
     KILN_WAIT_VMCNT(0);  // drain the re-fetch DMAs before the workgroup's LDS is reused or released
     if (p.ksplit <= 1 && p.store_rows) {
         __builtin_amdgcn_s_barrier();  // every wave is done with the ring: its LDS now stages the output rows

@@ -236,6 +236,31 @@ def test_edge_shapes(gpu, Tq, Tk, npad):
     assert_close(out.cpu().numpy(), ref, f"edge Tq={Tq} Tk={Tk} npad={npad}")
 
 
+@pytest.mark.parametrize("Tq,Tk,packed", [(200, 77, False), (130, 33, True), (64, 1, False), (257, 4000, True),
+                                           (129, 64, True)])
+def test_f16_kv_rows_past_tk_unread(gpu, Tq, Tk, packed):
+    """fp16 K/V whose rows after the last key hold NaN: the prepare pass must zero-fill the ragged last half tile
+    instead of reading them (a NaN there, weighted by P = 0, would still give NaN). packed: K and V are column
+    slices of one [rows, 3 x 2048] buffer (row stride 6144, as a fused QKV projection writes them)."""
+    q, k, v = (f16_round(t) for t in _qkv(57 + Tk, Tq, Tk, scale_qk=1.0))
+    ref = oracle.attn_f64(q.numpy(), k.numpy(), v.numpy(), H)
+    rows = Tk + 40
+    if packed:
+        buf = torch.full((rows, 3 * H * D), float("nan"), dtype=torch.float16, device=DEV)
+        buf[:Tk, :H * D] = k.half().to(DEV)
+        buf[:Tk, 2 * H * D:] = v.half().to(DEV)
+        kd, vd = buf[:, :H * D], buf[:, 2 * H * D:]
+    else:
+        kd = torch.full((rows, H * D), float("nan"), dtype=torch.float16, device=DEV)
+        vd = torch.full((rows, H * D), float("nan"), dtype=torch.float16, device=DEV)
+        kd[:Tk] = k.half().to(DEV)
+        vd[:Tk] = v.half().to(DEV)
+    out = torch.empty(Tq, H * D, dtype=torch.float32, device=DEV)
+    kiln_amd.attn_f16in(out, q.half().to(DEV), kd, vd, 1, Tq, Tk, H)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, f"K/V past Tk Tq={Tq} Tk={Tk} packed={packed}")
+
+
 def test_explicit_zero_keys_equal_npad(gpu):
     """npad analytic zero keys == the same zero rows present explicitly (tcflash.cuh:136-147)."""
     Tq, L, npad = 200, 40, 88

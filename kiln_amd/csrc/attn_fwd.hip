@@ -6,7 +6,8 @@
 // accumulator) instead of the reference's GeForce-specific fp16 partial sums.
 //
 // Design (gfx950, wave64):
-//  * workgroup = 4 waves x 32 query rows (BM = 128); K/V stream in half tiles of 32 keys.
+//  * workgroup = 4 waves x 32 query rows (BM = 128, two workgroups per CU), or 8 waves x 32 rows (one per CU,
+//    for grids whose 256-row tiles fill whole rounds of CUs); K/V stream in half tiles of 32 keys.
 //  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (under the chip's power limit
 //    this shape sustains more flop/s than 32x32x16): a wave's 32 rows are two 16-column query blocks, and
 //    the four lanes n, n+16, n+32, n+48 of a column hold 8 of each half tile's 32 keys, so the row sum needs
@@ -276,8 +277,9 @@ __device__ __forceinline__ void epilogue_rows(const AttnParams& p, const AttnJob
 
 // ------------------------------------------------------------------------------------------------
 // The kernel. A wave owns two query blocks of 16 rows (32 rows), a workgroup NW = 4 waves (BM = 128 rows), two
-// workgroups per CU (two waves per SIMD). NS = 4 ring stages (64 KB of LDS per workgroup; five measured the same
-// on long units and slower on short ones, whose prologue fills the ring). All products on v_mfma_f32_16x16x32_f16.
+// workgroups per CU (two waves per SIMD), NS = 4 ring stages (64 KB of LDS per workgroup; five measured the same
+// on long units and slower on short ones, whose prologue fills the ring); or 8 waves (256 rows), one workgroup per
+// CU, NS8 = 8 stages (128 KB). All products on v_mfma_f32_16x16x32_f16.
 //
 // Keys stream in 32-key half tiles (16 KB: K 8 KB + V 8 KB) through an NS-stage LDS ring filled by
 // direct global->LDS DMA (buffer_load_dwordx4 ... lds: no staging registers, no ds_write), NS-2 half
@@ -295,15 +297,23 @@ __device__ __forceinline__ void epilogue_rows(const AttnParams& p, const AttnJob
 // a scheduling fence: keeps the phases of a step in the order written and bounds the live registers
 #define KILN_FENCE() __builtin_amdgcn_sched_barrier(0)
 typedef __attribute__((address_space(3))) half8 lds_half8;
-constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = 4;
+constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = 4, NS8 = 8;
 constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
 static_assert(DMA_PER_HT == 4, "a wave copies four 1 KB pieces of each half tile");
 constexpr int PART_FLOATS = BM * HD + 2 * BM;      // one key range's partial result of a query tile
 static_assert(NS == 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration); half tile j in stage j % 4");
 
-template <typename InT, typename OutT, bool QNORM, bool ROPE>
-__global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 2nd: waves per SIMD
+// NWT waves per workgroup: 4 (two workgroups per CU, a 4-stage ring each) or 8 (one workgroup per CU, 256 query
+// rows sharing one 8-stage ring: half the K/V DMA, L2 reads and LDS writes per flop, which the power-limited
+// chip turns into clock).
+template <typename InT, typename OutT, bool QNORM, bool ROPE, int NWT>
+__global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams p) {  // 2nd: workgroups per CU
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];  // NS x 16 KB
+    constexpr int KBM = NWT * 32;                          // query rows of the workgroup
+    constexpr int KDMA = HT_H * 2 / 16 / (NWT * 64);      // 16-byte DMA pieces per thread per half tile
+    static_assert(NWT == 4 || NWT == 8, "4 or 8 waves");
+    constexpr int KNS = NWT == 8 ? NS8 : NS;               // ring stages (half tile j in stage j % KNS)
+    static_assert(KNS == 4 || KNS == 8, "a power of two: stage = j & (KNS - 1)");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4;  // 16-lane row of the wave: keys 4g..4g+3 of a key block, dims 8g.. of a d chunk
@@ -328,14 +338,16 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
     // Wave w copies the contiguous 4 KB [4w, 4w + 4) KB of the half tile in four 1 KB pieces: one M0 (LDS base)
     // and one soffset serve all four, the piece offset is the instruction's immediate (it applies to the global
     // and the LDS address alike).
-    const uint32_t dma_off = (uint32_t)wv * (DMA_PER_HT * 1024) + lane * 16;
+    const uint32_t dma_off = (uint32_t)wv * (KDMA * 1024) + lane * 16;
     auto dma = [&](int jh, int stage) {
-        auto* dst = (__attribute__((address_space(3))) void*)(lds + stage * HT_H + wv * (DMA_PER_HT * 512));
+        auto* dst = (__attribute__((address_space(3))) void*)(lds + stage * HT_H + wv * (KDMA * 512));
         const int so = (h0 + jh) * (HT_H * 2);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 1024, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 2048, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 3072, 0);
+        if constexpr (KDMA == 4) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 2048, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kv_rsrc, dst, 16, dma_off, so, 3072, 0);
+        }
     };
     // operand reads through 32-bit LDS byte addresses: base + immediate offsets fold into ds_read_b128
     auto kptr = [&](int stage) {
@@ -347,21 +359,24 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         return fmaxf(fmaxf(x0, x1), fmaxf(b[2], b[3]));
     };
 
-    // prologue: half tiles 0 .. NS-2 in flight, then the Q tile loads (their latencies overlap); wait for
-    // tiles 0 and 1
+    // prologue: half tiles 0 .. 2 in flight, then the Q tile loads (their latencies overlap), then the rest of a
+    // deeper ring (after the Q math, which waits for every vector memory operation issued before its loads);
+    // wait for tiles 0 and 1
 #pragma unroll
-    for (int i = 0; i < NS - 1; i++) dma(min(i, nh - 1), i);
+    for (int i = 0; i < 3; i++) dma(min(i, nh - 1), i);
     __builtin_amdgcn_sched_barrier(0);
     int row[2];
     bool qin[2];
     half8 qreg[2][4];
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
-        row[qb] = W.qt * BM + wv * 32 + 16 * qb + (lane & 15);
+        row[qb] = W.qt * KBM + wv * 32 + 16 * qb + (lane & 15);
         qin[qb] = row[qb] < p.Tq;
     }
     load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, g, qreg);
-    KILN_WAIT_VMCNT((NS - 3) * DMA_PER_HT);
+#pragma unroll
+    for (int i = 3; i < KNS - 1; i++) dma(min(i, nh - 1), i);
+    KILN_WAIT_VMCNT((KNS - 3) * KDMA);
     __builtin_amdgcn_s_barrier();
 
     floatx4 o[2][8];  // O^T per query block: d block db holds d = 16*db + 4g + i
@@ -406,7 +421,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         }
     }
 #pragma unroll
-    for (int s = 0; s < 4; s++) ka[s] = kptr(1 % NS)[s * 64];
+    for (int s = 0; s < 4; s++) ka[s] = kptr(1)[s * 64];
     // Enter the loop with no LDS read in flight: the loop body's first MFMA then waits only for the reads
     // of the previous iteration, and the waitcnt pass keeps the step's own new reads in flight.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -436,8 +451,17 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         return __builtin_amdgcn_ballot_w64(need) != 0;
     };
 
-    auto stage = [](int jh) { return jh & (NS - 1); };  // LDS stage of half tile jh
+    auto stage = [](int jh) { return jh & (KNS - 1); };  // LDS stage of half tile jh
     // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
+    // tile j+2 landed in every wave; every wave is done with tile j-1, whose stage is refilled. Only tiles
+    // j+3 .. j+NS-2 may be in flight; the peeled masking step (whose register spills, if any, are vector memory
+    // operations too) waits for everything.
+    auto sync_refill = [&](auto maskn_tag, int j) {
+        if constexpr (decltype(maskn_tag)::value) KILN_WAIT_VMCNT(0);
+        else KILN_WAIT_VMCNT((KNS - 4) * KDMA);
+        __builtin_amdgcn_s_barrier();
+        dma(min(j + KNS - 1, nh - 1), stage(j + KNS - 1));  // into the stage of tile j-1
+    };
     auto step = [&](auto maskn_tag, int j, floatx4 (&cur)[2][2], floatx4 (&sn)[2][2]) {
         constexpr bool MASKN = decltype(maskn_tag)::value;
         if (need_rescale()) rescale(cur);  // lazy rescale (rare)
@@ -470,13 +494,7 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         }
         KILN_FENCE();
 
-        // tile j+2 landed in every wave; every wave is done with tile j-1. Only tiles j+3 .. j+NS-2 may be
-        // in flight; the peeled masking step (whose register spills, if any, are vector memory operations
-        // too) waits for everything.
-        if constexpr (MASKN) KILN_WAIT_VMCNT(0);
-        else KILN_WAIT_VMCNT((NS - 4) * DMA_PER_HT);
-        __builtin_amdgcn_s_barrier();
-        dma(min(j + NS - 1, nh - 1), stage(j + NS - 1));  // into the stage of tile j-1
+        sync_refill(maskn_tag, j);
         half8 vb[4];
         {
             const lds_half8* kp = kptr(stage(j + 2));  // K_{j+2}; past the end: stale, unused
@@ -559,12 +577,12 @@ __global__ __launch_bounds__(NTHR, 2) void k_attn_fwd(const AttnParams p) {  // 
         OutT* stg = reinterpret_cast<OutT*>(lds) + wv * 16 * ORS<OutT>;
 #pragma unroll
         for (int qb = 0; qb < 2; qb++)
-            epilogue_rows<OutT>(p, J, W.qt * BM + wv * 32 + 16 * qb, W.h, g, lane, m[qb], l[qb], o[qb], stg);
+            epilogue_rows<OutT>(p, J, W.qt * KBM + wv * 32 + 16 * qb, W.h, g, lane, m[qb], l[qb], o[qb], stg);
         return;
     }
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
-        if (p.ksplit > 1) {  // partial result of this key range: unnormalized O, running max m, row sum l
+        if (NWT == 4 && p.ksplit > 1) {  // partial result of this key range: unnormalized O, running max m, row sum l
             const int unit = (W.jb * p.H + W.h) * p.qtiles + W.qt;
             float* po = p.part + (size_t)(unit * p.ksplit + W.ks) * PART_FLOATS;
             const int r = wv * 32 + 16 * qb + (lane & 15);
@@ -800,15 +818,28 @@ size_t attn_split_bytes(int ksplit, int njobs, int Tq, int H) {
     if (ksplit <= 1) return 0;
     return (size_t)((Tq + BM - 1) / BM) * H * njobs * ksplit * PART_FLOATS * sizeof(float);
 }
-template <typename InT, typename OutT, bool QN, bool RP>
-static hipError_t launch_sel(AttnParams p, int Tq, int units, hipStream_t s) {
-    p.qtiles = (Tq + BM - 1) / BM;
+template <typename InT, typename OutT, bool QN, bool RP, int NWT>
+static hipError_t launch_nw(AttnParams& p, int Tq, int units, hipStream_t s) {
+    constexpr int KBM = NWT * 32;
+    p.qtiles = (Tq + KBM - 1) / KBM;
     p.total = p.qtiles * units * p.ksplit;
     const int nb = (p.total + 7) / 8 * 8;
     p.per = nb / 8;
-    auto kern = k_attn_fwd<InT, OutT, QN, RP>;
-    const size_t lds = (size_t)NS * HT_H * sizeof(_Float16);
-    hipLaunchKernelGGL(kern, dim3(nb), dim3(NTHR), lds, s, p);
+    auto kern = k_attn_fwd<InT, OutT, QN, RP, NWT>;
+    // the ring, or the output staging of 16 rows per wave if that is larger (8 waves, fp32 output)
+    const size_t lds = std::max((size_t)(NWT == 8 ? NS8 : NS) * HT_H * sizeof(_Float16), (size_t)NWT * 16 * ORS<OutT> * sizeof(OutT));
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(NWT * 64), lds, s, p);
+    return hipGetLastError();
+}
+template <typename InT, typename OutT, bool QN, bool RP>
+static hipError_t launch_sel(AttnParams p, int Tq, int units, hipStream_t s) {
+    // 8-wave workgroups where 256-row query tiles give every CU whole rounds of work (config 4: 512 tiles on 256
+    // CUs); elsewhere the 128-row tiles fill the chip more evenly (and key-split launches need them)
+    const long t8 = (long)((Tq + 255) / 256) * units;
+    const int cus = resident_slots() / 2;
+    if (p.ksplit <= 1 && cus > 0 && t8 % cus == 0) return launch_nw<InT, OutT, QN, RP, 8>(p, Tq, units, s);
+    hipError_t e = launch_nw<InT, OutT, QN, RP, 4>(p, Tq, units, s);
+    if (e != hipSuccess) return e;
     if (p.ksplit > 1) hipLaunchKernelGGL(k_attn_merge<OutT>, dim3(4 * p.qtiles * units), dim3(256), 0, s, p);
     return hipGetLastError();
 }

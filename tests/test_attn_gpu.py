@@ -261,6 +261,26 @@ def test_f16_kv_rows_past_tk_unread(gpu, Tq, Tk, packed):
     assert_close(out.cpu().numpy(), ref, f"K/V past Tk Tq={Tq} Tk={Tk} packed={packed}")
 
 
+@pytest.mark.parametrize("Tq,Tk,B,npad,od", [(1000, 333, 4, 5, torch.float32), (2000, 777, 2, 0, torch.float16),
+                                           (1793, 64, 2, 3, torch.float32), (769, 1, 4, 0, torch.float16)])
+def test_eight_wave_workgroups(gpu, Tq, Tk, B, npad, od):
+    """Grids whose 256-row query tiles fill whole rounds of CUs (ceil(Tq / 256) x H x B a multiple of the CU count,
+    as at config 4) run the 8-wave kernel (one workgroup per CU, 8-stage ring): ragged query and key tiles, npad,
+    both output types, batched items."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if ((Tq + 255) // 256) * H * B % cus:
+        pytest.skip(f"shape does not select the 8-wave kernel on {cus} CUs")
+    q, k, v = (f16_round(randn(71 + i, B * T, H * D)) for i, T in enumerate((Tq, Tk, Tk)))
+    out = torch.full((B * Tq, H * D), float("nan"), dtype=od, device=DEV)
+    kiln_amd.attn_f16in(out, q.half().to(DEV), k.half().to(DEV), v.half().to(DEV), B, Tq, Tk, H, npad=npad)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    for b in range(B):
+        ref = oracle.attn_f64(q[b * Tq:(b + 1) * Tq].numpy(), k[b * Tk:(b + 1) * Tk].numpy(),
+                              v[b * Tk:(b + 1) * Tk].numpy(), H, npad=npad)
+        assert_close(o[b * Tq:(b + 1) * Tq], ref, f"8 waves Tq={Tq} Tk={Tk} b={b} npad={npad} out={od}")
+
+
 def test_explicit_zero_keys_equal_npad(gpu):
     """npad analytic zero keys == the same zero rows present explicitly (tcflash.cuh:136-147)."""
     Tq, L, npad = 200, 40, 88

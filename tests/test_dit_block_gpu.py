@@ -314,12 +314,13 @@ def test_step_cache_skip_reuses_residual(gpu):
     np.testing.assert_array_equal(y.cpu().numpy(), (a - b).numpy())
 
 
-@pytest.mark.parametrize("Hh,Hp_,Wp_,Bb", [(4, 8, 12, 2), (2, 10, 10, 3), (16, 48, 72, 2)])
+@pytest.mark.parametrize("Hh,Hp_,Wp_,Bb", [(4, 8, 12, 2), (2, 10, 10, 3), (16, 48, 72, 2), (16, 32, 60, 2)])
 def test_dit_self_attn_x16_fused_projection(gpu, Hh, Hp_, Wp_, Bb):
     """kiln_dit_self_attn_x16 (QKV GEMM whose epilogue does QK-RMSNorm, RoPE and the K/V preparation) against
     the float64 statement of dit.cu:460-469 on sampled rows (BASELINE bar: max-abs 2e-3, mean-abs 2e-4), and
     against the unfused path (linear16 F32 + kiln_dit_self_attn_fused) on every output. T = 100 has a partial
-    last key tile; T = 3456 x 16 heads is config 5's shape."""
+    last key tile; T = 3456 x 16 heads is config 5's shape; T = 1920 x 16 heads x 2 items gives 256 query tiles
+    of 256 rows, which on a 256-CU part selects the 8-wave attention kernel for both paths."""
     Dd, Tt = Hh * HD, Hp_ * Wp_
     g = torch.Generator().manual_seed(34 + Hh)
     x = (torch.randn(Bb * Tt, Dd, generator=g)).half()

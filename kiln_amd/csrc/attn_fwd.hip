@@ -297,9 +297,7 @@ __device__ __forceinline__ void epilogue_rows(const AttnParams& p, const AttnJob
 // a scheduling fence: keeps the phases of a step in the order written and bounds the live registers
 #define KILN_FENCE() __builtin_amdgcn_sched_barrier(0)
 typedef __attribute__((address_space(3))) half8 lds_half8;
-constexpr int NW = 4, NTHR = NW * 64, BM = NW * 32, NS = 4, NS8 = 8;
-constexpr int DMA_PER_HT = HT_H * 2 / 16 / NTHR;  // 16-byte DMA pieces per thread per half tile
-static_assert(DMA_PER_HT == 4, "a wave copies four 1 KB pieces of each half tile");
+constexpr int NW = 4, BM = NW * 32, NS = 4, NS8 = 8;  // the 4-wave form's geometry (key-split partials use BM)
 constexpr int PART_FLOATS = BM * HD + 2 * BM;      // one key range's partial result of a query tile
 static_assert(NS == 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this iteration); half tile j in stage j % 4");
 
@@ -329,15 +327,15 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
     const _Float16* kvh = reinterpret_cast<const _Float16*>(J.kv) + (size_t)W.h * kv_head_stride(Tk);
     const uint32_t lds_base = (uint32_t)(size_t)(__attribute__((address_space(3))) _Float16*)lds;
 
-    // half tile jh -> stage: this thread's 16-byte pieces tid + NTHR*i; the wave's 64 lanes write 1 KB
+    // half tile jh -> stage: each wave copies KDMA 16-byte pieces per lane; the wave's 64 lanes write 1 KB
     // of contiguous LDS at the wave-uniform base the DMA takes from M0.
     // Buffer-form DMA: the lane offset tid*16 is a constant VGPR; the half tile and piece offsets go in the
     // SGPR soffset, so a refill costs no vector instructions. The descriptor's range is the head's K/V block.
     const __amdgpu_buffer_rsrc_t kv_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(kvh), (short)0, (int)(kv_head_stride(Tk) * 2), 0x00020000 /* raw, CDNA */);
-    // Wave w copies the contiguous 4 KB [4w, 4w + 4) KB of the half tile in four 1 KB pieces: one M0 (LDS base)
-    // and one soffset serve all four, the piece offset is the instruction's immediate (it applies to the global
-    // and the LDS address alike).
+    // Wave w copies the contiguous KDMA KB [KDMA w, KDMA (w + 1)) KB of the half tile (4 KB with 4 waves, 2 KB with
+    // 8) in 1 KB pieces: one M0 (LDS base) and one soffset serve all of them, the piece offset is the instruction's
+    // immediate (it applies to the global and the LDS address alike).
     const uint32_t dma_off = (uint32_t)wv * (KDMA * 1024) + lane * 16;
     auto dma = [&](int jh, int stage) {
         auto* dst = (__attribute__((address_space(3))) void*)(lds + stage * HT_H + wv * (KDMA * 512));

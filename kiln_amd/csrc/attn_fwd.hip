@@ -10,8 +10,9 @@
 //    for grids whose 256-row tiles fill whole rounds of CUs); K/V stream in half tiles of 32 keys.
 //  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (under the chip's power limit
 //    this shape sustains more flop/s than 32x32x16): a wave's 32 rows are two 16-column query blocks, and
-//    the four lanes n, n+16, n+32, n+48 of a column hold 8 of each half tile's 32 keys, so the row sum needs
-//    no cross-lane step until the epilogue and the row max one only when the running max moves.
+//    the four lanes n, n+16, n+32, n+48 of a column hold 8 of each half tile's 32 keys, so the row max needs
+//    a cross-lane step only when the running max moves; the row sum comes from the matrix core (P^T times an
+//    all-ones block).
 //  * O^T = V^T P^T: P^T comes straight out of the two S^T accumulators of a query block (no LDS round trip);
 //    V^T is the A operand, pre-permuted by the K/V prepare pass so that every LDS operand read of a wave is
 //    one contiguous, conflict-free 1 KB ds_read_b128, and each read feeds both query blocks.
@@ -289,9 +290,9 @@ __device__ __forceinline__ void epilogue_rows(const AttnParams& p, const AttnJob
 // Software pipeline, per half tile j (S_j - m and max(S_j) - m in registers, K_{j+1} d chunks 0-1 in
 // registers, half tiles j .. j+NS-3 resident or in flight):
 //   [rare: rescale O, l, m]                                         (the only branch)
-//   K_{j+1} chunks 2-3, V_j[db 0-3] reads | QK_{j+1} MFMAs interleaved with exp/cvt/row-sum of S_j |
+//   K_{j+1} chunks 2-3, V_j[db 0-3] reads | QK_{j+1} MFMAs interleaved with exp/cvt of S_j |
 //   wait tile j+2, barrier | DMA tile j+NS-1 into the stage of tile j-1 | K_{j+2} chunks 0-1, V_j[db 4-7] reads |
-//   PV_j MFMAs interleaved with max(S_{j+1})
+//   PV_j and row-sum MFMAs interleaved with max(S_{j+1})
 // Every read of a stage completes before the barrier that precedes its refill.
 // ------------------------------------------------------------------------------------------------
 // a scheduling fence: keeps the phases of a step in the order written and bounds the live registers
@@ -450,9 +451,8 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
     };
 
     auto stage = [](int jh) { return jh & (KNS - 1); };  // LDS stage of half tile jh
-    // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
-    // tile j+2 landed in every wave; every wave is done with tile j-1, whose stage is refilled. Only tiles
-    // j+3 .. j+NS-2 may be in flight; the peeled masking step (whose register spills, if any, are vector memory
+    // Tile j+2 landed in every wave; every wave is done with tile j-1, whose stage is refilled. Only tiles
+    // j+3 .. j+KNS-2 may be in flight; the peeled masking step (whose register spills, if any, are vector memory
     // operations too) waits for everything.
     auto sync_refill = [&](auto maskn_tag, int j) {
         if constexpr (decltype(maskn_tag)::value) KILN_WAIT_VMCNT(0);
@@ -460,6 +460,7 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
         __builtin_amdgcn_s_barrier();
         dma(min(j + KNS - 1, nh - 1), stage(j + KNS - 1));  // into the stage of tile j-1
     };
+    // One half tile j with a successor. MASKN: the successor is the last half tile and ragged.
     auto step = [&](auto maskn_tag, int j, floatx4 (&cur)[2][2], floatx4 (&sn)[2][2]) {
         constexpr bool MASKN = decltype(maskn_tag)::value;
         if (need_rescale()) rescale(cur);  // lazy rescale (rare)

@@ -61,6 +61,39 @@ def _split_cases(n=8, seed=77):
 SPLIT_CASES = _split_cases()
 
 
+def _wide_cases(n=8, seed=4242):
+    """Grids of 256-row query tiles that fill whole rounds of a 256-CU part (tiles x H x B = 256 or 512), which
+    run the 8-wave kernel: every route, ragged query and key counts, npad, padded strides and offsets."""
+    rng = np.random.default_rng(seed)
+    shapes = [(16, 1, 16), (16, 2, 8), (32, 1, 8), (8, 4, 8), (16, 4, 4), (16, 2, 16)]  # (H, B, query tiles)
+    out = []
+    for i in range(n):
+        route = ["f32out", "f16out", "f16in", "dit"][i % 4]
+        H, B, nt = shapes[int(rng.integers(0, len(shapes)))]
+        if route in ("f32out", "f16out"):  # single-item routes: H x tiles must fill the rounds alone
+            H, B, nt = (16, 1, 16) if i % 2 == 0 else (32, 1, 8)
+        if route == "dit":  # the oracle's full-row reference: keep T x T x B small
+            H, B, nt = [(16, 4, 4), (16, 2, 8), (8, 4, 8)][i % 3]
+        c = dict(route=route, H=H, B=B, pad=[int(rng.choice([0, 8, 24])) for _ in range(4)],
+                 off=int(rng.choice([0, 8])), seed=7000 + i)
+        lo, hi = 256 * (nt - 1) + 1, 256 * nt
+        if route == "dit":
+            Wp = int(rng.integers(24, 48))
+            Hp = -(-lo // Wp)  # smallest Hp with Hp * Wp in the tile range
+            if Hp * Wp > hi:
+                Hp, Wp = nt * 8, 32  # T = 256 nt
+            c.update(Hp=Hp, Wp=Wp, f32=bool(rng.integers(0, 2)), out32=bool(rng.integers(0, 2)))
+        else:
+            c.update(Tq=int(rng.integers(lo, hi + 1)), Tk=int(rng.integers(1, 1200)),
+                     npad=int(rng.choice([0, int(rng.integers(1, 300))])), out32=bool(rng.integers(0, 2)),
+                     causal=False)
+        out.append(c)
+    return out
+
+
+WIDE_CASES = _wide_cases()
+
+
 def _strided(rows, H, pad, off, dtype, data):
     """[rows, H*D] view of a [rows, off + H*D + pad] buffer (row stride = off + H*D + pad), holding data."""
     buf = torch.zeros(rows, off + H * D + pad, dtype=dtype, device=DEV)
@@ -78,6 +111,11 @@ def test_random_shapes(gpu, idx):
 @pytest.mark.parametrize("idx", range(len(SPLIT_CASES)))
 def test_random_split_shapes(gpu, idx):
     _run_case(SPLIT_CASES[idx], 100 + idx)
+
+
+@pytest.mark.parametrize("idx", range(len(WIDE_CASES)))
+def test_random_eight_wave_shapes(gpu, idx):
+    _run_case(WIDE_CASES[idx], 200 + idx)
 
 
 def _run_case(c, idx):

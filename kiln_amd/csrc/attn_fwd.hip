@@ -833,10 +833,15 @@ static hipError_t launch_nw(AttnParams& p, int Tq, int units, hipStream_t s) {
 template <typename InT, typename OutT, bool QN, bool RP>
 static hipError_t launch_sel(AttnParams p, int Tq, int units, hipStream_t s) {
     // 8-wave workgroups where 256-row query tiles give every CU whole rounds of work (config 4: 512 tiles on 256
-    // CUs); elsewhere the 128-row tiles fill the chip more evenly (and key-split launches need them)
+    // CUs), or at least one round of long units (keys >= 2048: config 5's self-attention, 448 tiles, whose 4-wave
+    // form also needs two full rounds); elsewhere the 128-row tiles fill the chip more evenly and short units pay
+    // less prologue per flop (and key-split launches need them)
     const long t8 = (long)((Tq + 255) / 256) * units;
     const int cus = resident_slots() / 2;
-    if (p.ksplit <= 1 && cus > 0 && t8 % cus == 0) return launch_nw<InT, OutT, QN, RP, 8>(p, Tq, units, s);
+    bool longk = true;
+    for (int i = 0; i < p.njobs; i++) longk &= p.job[i].Tk >= 2048;
+    if (p.ksplit <= 1 && cus > 0 && (t8 % cus == 0 || (longk && t8 >= cus)))
+        return launch_nw<InT, OutT, QN, RP, 8>(p, Tq, units, s);
     hipError_t e = launch_nw<InT, OutT, QN, RP, 4>(p, Tq, units, s);
     if (e != hipSuccess) return e;
     if (p.ksplit > 1) hipLaunchKernelGGL(k_attn_merge<OutT>, dim3(4 * p.qtiles * units), dim3(256), 0, s, p);

@@ -262,13 +262,16 @@ def test_f16_kv_rows_past_tk_unread(gpu, Tq, Tk, packed):
 
 
 @pytest.mark.parametrize("Tq,Tk,B,npad,od", [(1000, 333, 4, 5, torch.float32), (2000, 777, 2, 0, torch.float16),
-                                           (1793, 64, 2, 3, torch.float32), (769, 1, 4, 0, torch.float16)])
+                                           (1793, 64, 2, 3, torch.float32), (769, 1, 4, 0, torch.float16),
+                                           (1100, 2100, 4, 7, torch.float16)])
 def test_eight_wave_workgroups(gpu, Tq, Tk, B, npad, od):
     """Grids whose 256-row query tiles fill whole rounds of CUs (ceil(Tq / 256) x H x B a multiple of the CU count,
-    as at config 4) run the 8-wave kernel (one workgroup per CU, 8-stage ring): ragged query and key tiles, npad,
-    both output types, batched items."""
+    as at config 4), or at least one round with keys >= 2048 (as config 5's self-attention), run the 8-wave kernel
+    (one workgroup per CU, 8-stage ring): ragged query and key tiles, a half-empty last round, npad, both output
+    types, batched items."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    if ((Tq + 255) // 256) * H * B % cus:
+    t8 = ((Tq + 255) // 256) * H * B
+    if t8 % cus and not (Tk >= 2048 and t8 >= cus):
         pytest.skip(f"shape does not select the 8-wave kernel on {cus} CUs")
     q, k, v = (f16_round(randn(71 + i, B * T, H * D)) for i, T in enumerate((Tq, Tk, Tk)))
     out = torch.full((B * Tq, H * D), float("nan"), dtype=od, device=DEV)

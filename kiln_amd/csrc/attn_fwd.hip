@@ -7,7 +7,8 @@
 //
 // Design (gfx950, wave64):
 //  * workgroup = 4 waves x 32 query rows (BM = 128, two workgroups per CU), or 8 waves x 32 rows (one per CU,
-//    for grids whose 256-row tiles fill whole rounds of CUs); K/V stream in half tiles of 32 keys.
+//    for grids whose 256-row tiles fill whole rounds of CUs, or at least one round of units with >= 2048 keys);
+//    K/V stream in half tiles of 32 keys.
 //  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (under the chip's power limit
 //    this shape sustains more flop/s than 32x32x16): a wave's 32 rows are two 16-column query blocks, and
 //    the four lanes n, n+16, n+32, n+48 of a column hold 8 of each half tile's 32 keys, so the row max needs

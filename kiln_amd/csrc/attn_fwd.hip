@@ -162,13 +162,16 @@ __device__ __forceinline__ void load_q(const AttnParams& p, const void* q, const
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    // Rows past Tq (which read row 0) are zeroed by the final multiplier; the norm's per-row factor r joins the
+    // pre-scale there: q' = RoPE(x * w) * (r * qscale), the same mathematics as RoPE(x * r * w) * qscale.
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
         float x[4][8];
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[c][e] = qin[qb] ? raw[qb][c][e] : 0.f;
+            for (int e = 0; e < 8; e++) x[c][e] = raw[qb][c][e];
+        float sc = p.qscale;
         if constexpr (QNORM) {
             float ss = 0.f;
 #pragma unroll
@@ -176,12 +179,13 @@ __device__ __forceinline__ void load_q(const AttnParams& p, const void* q, const
 #pragma unroll
                 for (int e = 0; e < 8; e++) ss += x[c][e] * x[c][e];
             ss = quad_sum(ss);
-            const float r = rsqrtf(ss * (1.0f / HD) + p.eps);
+            sc *= rsqrtf(ss * (1.0f / HD) + p.eps);
 #pragma unroll
             for (int c = 0; c < 4; c++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) x[c][e] = x[c][e] * r * bf16_to_f32(wb[c][e]);
+                for (int e = 0; e < 8; e++) x[c][e] *= bf16_to_f32(wb[c][e]);
         }
+        sc = qin[qb] ? sc : 0.f;
         if constexpr (ROPE) {
 #pragma unroll
             for (int c = 0; c < 2; c++)
@@ -196,7 +200,7 @@ __device__ __forceinline__ void load_q(const AttnParams& p, const void* q, const
 #pragma unroll
         for (int c = 0; c < 4; c++) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[c][e] *= p.qscale;
+            for (int e = 0; e < 8; e++) x[c][e] *= sc;
             qreg[qb][c] = to_half8(x[c]);
         }
     }

@@ -38,8 +38,9 @@ class Scope {
     Scope& operator=(const Scope&) = delete;
 
    private:
-    int slot_ = -1;
-    bool nested_ = false;
+    int slot_ = -1;          // the event pair recording this scope, or -1
+    unsigned gen_ = 0;       // the profile generation the slot belongs to (kiln_prof_enable starts a new one)
+    bool counted_ = false;   // this scope raised the thread's nesting depth and lowers it again
     hipStream_t s_ = nullptr;
 };
 }  // namespace kiln::prof

@@ -334,23 +334,48 @@ __global__ void k_gelu(float* __restrict__ x, size_t n) {
     }
 }
 
-// er_sde step (pipeline.cu:345-359): x <- a x + b den (+ c2 dd (+ c3 (dd - oldd) inv3) from stage 2, with
-// dd = (den - old) inv2, which is kept in oldd for the next step) (+ cn noise)
+// er_sde update of the latent (the per-element part of pipeline.cu:345-359; weights from the host): with the
+// first divided difference D1 = (den - old) d1_inv, which is also kept for the next step, and the second
+// D2 = (D1 - D1_prev) d2_inv,
+//   x <- x_w x + den_w den [+ d1_w D1 [+ d2_w D2]] [+ noise_w noise]
+// ORDER (1-3) selects the terms at compile time. Four elements per thread through 16-byte accesses; the
+// launcher takes this form only when every array is 16-byte aligned, and a second launch covers n % 4.
+struct ErSdeW {
+    float x_w, den_w, d1_w, d1_inv, d2_w, d2_inv, noise_w;
+};
+template <int ORDER, bool NOISE, int V>
 __global__ void k_flow_ersde(float* __restrict__ x, const float* __restrict__ den, const float* __restrict__ old,
-                             float* __restrict__ oldd, const float* __restrict__ noise, float a, float b, float c2,
-                             float inv2, float c3, float inv3, float cn, int stage, size_t n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float d = den[i];
-    float v = a * x[i] + b * d;
-    if (stage >= 2) {
-        const float dd = (d - old[i]) * inv2;
-        v += c2 * dd;
-        if (stage >= 3) v += c3 * (dd - oldd[i]) * inv3;
-        oldd[i] = dd;
+                             float* __restrict__ d1_keep, const float* __restrict__ noise, const ErSdeW w, size_t nv) {
+    typedef float vec __attribute__((ext_vector_type(V)));
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nv) return;
+    const vec dv = reinterpret_cast<const vec*>(den)[t];
+    vec acc = reinterpret_cast<const vec*>(x)[t] * w.x_w + dv * w.den_w;
+    if constexpr (ORDER >= 2) {
+        const vec d1 = (dv - reinterpret_cast<const vec*>(old)[t]) * w.d1_inv;
+        acc += d1 * w.d1_w;
+        if constexpr (ORDER >= 3) acc += ((d1 - reinterpret_cast<const vec*>(d1_keep)[t]) * w.d2_inv) * w.d2_w;
+        reinterpret_cast<vec*>(d1_keep)[t] = d1;
     }
-    if (noise) v += cn * noise[i];
-    x[i] = v;
+    if constexpr (NOISE) acc += reinterpret_cast<const vec*>(noise)[t] * w.noise_w;
+    reinterpret_cast<vec*>(x)[t] = acc;
+}
+
+template <int ORDER, bool NOISE>
+static void launch_ersde_order(float* x, const float* den, const float* old, float* d1, const float* noise,
+                               const ErSdeW& w, size_t n, bool vec4, hipStream_t st) {
+    size_t done = 0;
+    if (vec4 && n >= 4) {
+        const size_t nv = n / 4;
+        hipLaunchKernelGGL((k_flow_ersde<ORDER, NOISE, 4>), dim3((unsigned)((nv + 255) / 256)), dim3(256), 0, st, x, den,
+                           old, d1, noise, w, nv);
+        done = nv * 4;
+    }
+    if (done < n) {
+        auto off = [&](auto* p) { return p ? p + done : p; };
+        hipLaunchKernelGGL((k_flow_ersde<ORDER, NOISE, 1>), dim3((unsigned)((n - done + 255) / 256)), dim3(256), 0, st,
+                           x + done, den + done, off(old), off(d1), off(noise), w, n - done);
+    }
 }
 
 static unsigned nblk(size_t n) { return (unsigned)((n + 255) / 256); }
@@ -545,8 +570,19 @@ hipError_t launch_rel_l1(const float* a, const float* b, size_t n, float* acc, h
 hipError_t launch_flow_ersde(float* x, const float* den, const float* old, float* oldd, const float* noise, float a,
                              float b, float c2, float inv2, float c3, float inv3, float cn, int stage, size_t n,
                              hipStream_t st) {
-    hipLaunchKernelGGL(k_flow_ersde, dim3(nblk(n)), dim3(256), 0, st, x, den, old, oldd, noise, a, b, c2, inv2, c3, inv3,
-                       cn, stage, n);
+    const ErSdeW w{a, b, c2, inv2, c3, inv3, cn};
+    bool vec4 = true;
+    for (const void* p : {(const void*)x, (const void*)den, (const void*)old, (const void*)oldd, (const void*)noise})
+        vec4 &= ((uintptr_t)p & 15) == 0;
+    const bool nz = noise != nullptr;
+    auto go = [&](auto order) {
+        constexpr int O = decltype(order)::value;
+        if (nz) launch_ersde_order<O, true>(x, den, old, oldd, noise, w, n, vec4, st);
+        else launch_ersde_order<O, false>(x, den, old, oldd, noise, w, n, vec4, st);
+    };
+    if (stage >= 3) go(std::integral_constant<int, 3>{});
+    else if (stage == 2) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 1>{});
     return hipGetLastError();
 }
 hipError_t launch_gelu(float* x, size_t n, hipStream_t st) {

@@ -26,30 +26,38 @@ std::atomic<bool> g_on{false};
 std::mutex g_mu;
 std::vector<Pair> g_pairs;  // the event pool; [0, g_used) hold this profile's scopes
 size_t g_used = 0;
+unsigned g_gen = 0;            // bumped by kiln_prof_enable: scopes of an earlier profile record nothing more
 thread_local int t_depth = 0;  // a scope inside another one (an entry point calling another) is not timed
 }  // namespace
 
+// The thread's depth counts every scope that was entered while profiling was on, timed or not, so that a failed
+// event call cannot leave the depth raised (which would make every later scope look nested).
 Scope::Scope(const char* name, hipStream_t s) {
     if (!g_on.load(std::memory_order_relaxed)) return;
-    nested_ = t_depth++ > 0;
-    if (nested_) return;
+    counted_ = true;
+    if (t_depth++ > 0) return;
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_used == g_pairs.size()) {
         Pair p{name};
-        if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) return;
+        if (hipEventCreate(&p.a) != hipSuccess) return;
+        if (hipEventCreate(&p.b) != hipSuccess) {
+            (void)hipEventDestroy(p.a);
+            return;
+        }
         g_pairs.push_back(p);
     }
+    if (hipEventRecord(g_pairs[g_used].a, s) != hipSuccess) return;
     slot_ = (int)g_used++;
     g_pairs[slot_].name = name;
+    gen_ = g_gen;
     s_ = s;
-    if (hipEventRecord(g_pairs[slot_].a, s) != hipSuccess) slot_ = -1;
 }
 
 Scope::~Scope() {
-    if (nested_ || slot_ >= 0) t_depth--;
+    if (counted_) t_depth--;
     if (slot_ < 0) return;
     std::lock_guard<std::mutex> lk(g_mu);
-    (void)hipEventRecord(g_pairs[slot_].b, s_);
+    if (gen_ == g_gen) (void)hipEventRecord(g_pairs[slot_].b, s_);  // a re-enabled profile may own the slot now
 }
 
 }  // namespace kiln::prof
@@ -59,6 +67,7 @@ extern "C" {
 int kiln_prof_enable(int on) {
     std::lock_guard<std::mutex> lk(kiln::prof::g_mu);
     kiln::prof::g_used = 0;
+    kiln::prof::g_gen++;
     kiln::prof::g_on = on != 0;
     return KILN_OK;
 }

@@ -29,7 +29,8 @@ int fail(int code, const std::string& msg) {
     return code;
 }
 
-// runs f, mapping exceptions to status codes
+// runs f, mapping exceptions to status codes: a kiln::Error keeps its own (HIP failure, device memory, a failed
+// library call), anything else is a bad argument
 template <typename F>
 int guarded(F&& f) {
     try {
@@ -37,6 +38,8 @@ int guarded(F&& f) {
         return KILN_OK;
     } catch (const kiln::Cancelled&) {
         return fail(KILN_ECANCELLED, "cancelled");
+    } catch (const kiln::Error& e) {
+        return fail(e.status, e.what());
     } catch (const std::bad_alloc&) {
         return fail(KILN_ENOMEM, "host out of memory");
     } catch (const std::exception& e) {
@@ -83,7 +86,7 @@ kiln::SampleParams params_of(const kiln_sample_params* p) {
 class CallbackModel : public kiln::VelocityModel {
    public:
     CallbackModel(kiln_velocity_fn fn, void* user) : fn_(fn), user_(user) {}
-    void forward(float* const* outs, const float* x, float t, bool cfg_now, bool cache_allow,
+    void forward(float* const* outs, const float* x, float sigma, float t, bool cfg_now, bool cache_allow,
                  bool* cache_skipped) override {
         int skipped = 0;
         if (fn_(user_, outs, x, t, cfg_now ? 1 : 0, cache_allow ? 1 : 0, &skipped) != 0)
@@ -233,18 +236,18 @@ int kiln_step_coef(const char* sampler, const float* sig, int nsig, int i, int h
     if (!sampler || !sig || !abc || i < 0 || i + 1 >= nsig || (have_old && i < 1))
         return fail(KILN_EINVAL, "step_coef: bad arguments");
     return guarded([&] {
-        const kiln::StepCoef c = kiln::step_coef(sampler, std::vector<float>(sig, sig + nsig), i, have_old != 0);
-        abc[0] = c.a, abc[1] = c.b, abc[2] = c.c;
+        const kiln::LinearStep w = kiln::linear_step(sampler, std::vector<float>(sig, sig + nsig), i, have_old != 0);
+        abc[0] = w.x_w, abc[1] = w.den_w, abc[2] = w.old_w;
     });
 }
 
 int kiln_ersde_coef(const float* sig, int nsig, int i, float* c7, int* stage) {
     if (!sig || !c7 || !stage || i < 0 || i + 1 >= nsig) return fail(KILN_EINVAL, "ersde_coef: bad arguments");
     return guarded([&] {
-        const kiln::ErSdeCoef c = kiln::ersde_coef(std::vector<float>(sig, sig + nsig), i);
-        const float v[7] = {c.a, c.b, c.c2, c.inv2, c.c3, c.inv3, c.cn};
+        const kiln::ErSdeStep e = kiln::ersde_step(std::vector<float>(sig, sig + nsig), i);
+        const float v[7] = {e.x_w, e.den_w, e.d1_w, e.d1_inv, e.d2_w, e.d2_inv, e.noise_w};
         for (int k = 0; k < 7; k++) c7[k] = v[k];
-        *stage = c.stage;
+        *stage = e.order;
     });
 }
 
@@ -288,7 +291,6 @@ int kiln_dit_sample(kiln_dit* dit, float* x, int Hl, int Wl, const kiln_dit_cont
         const kiln::SampleParams p = params_of(sp);
         kiln::DitVelocity m(dit->dit, Hl, Wl, pos->c.get(), neg ? neg->c.get() : nullptr, nag_of(nag), nag_sigma_end,
                             p.cache_threshold, batch_cfg != 0, fp32 != 0);
-        m.set_timestep_mult(p.timestep_mult);
         const kiln::SampleResult r = kiln::sample(m, x, Hl, Wl, neg != nullptr, p, init, mask,
                                                   step_fn(on_step, step_user), cancel_fn(cancel), dit->dit.stream());
         if (cache_skips) *cache_skips = r.cache_skips;

@@ -17,12 +17,12 @@ kiln_stream_t ks(hipStream_t s) { return (kiln_stream_t)s; }
 
 void ck(int rc, const char* what) {
     if (rc != KILN_OK)
-        throw std::runtime_error(std::string(what) + ": " + kiln_attn_status_string(rc) + " (" + kiln_attn_last_error() +
-                                 ")");
+        throw Error(rc, std::string(what) + ": " + kiln_attn_status_string(rc) + " (" + kiln_attn_last_error() + ")");
 }
 
 void ck_hip(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+    if (e != hipSuccess)
+        throw Error(e == hipErrorOutOfMemory ? KILN_ENOMEM : KILN_EHIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
 void DeviceBuffer::reserve(size_t bytes) {
@@ -53,7 +53,7 @@ void Arena::reserve(size_t bytes) {
 void* Arena::take(size_t bytes) {
     const size_t off = (top_ + 255) / 256 * 256;
     if (off + bytes > buf_.bytes())
-        throw std::runtime_error("arena: " + std::to_string(off + bytes) + " bytes needed, " +
+        throw Error(KILN_ENOMEM, "arena: " + std::to_string(off + bytes) + " bytes needed, " +
                                  std::to_string(buf_.bytes()) + " reserved");
     top_ = off + bytes;
     peak_ = std::max(peak_, top_);

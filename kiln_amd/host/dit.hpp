@@ -20,7 +20,14 @@
 
 namespace kiln {
 
-// Throws std::runtime_error with the library's message when a C-ABI call fails.
+// A failure that carries its kiln_status (KILN_EHIP for a HIP error, KILN_ENOMEM for device memory or an arena
+// that is too small, the library's own code for a failed C-ABI call), so the C ABI can hand it back unchanged.
+struct Error : std::runtime_error {
+    int status;
+    Error(int st, const std::string& msg) : std::runtime_error(msg), status(st) {}
+};
+
+// Throw kiln::Error with the library's message when a C-ABI call or a HIP call fails.
 void ck(int rc, const char* what);
 void ck_hip(hipError_t e, const char* what);
 

@@ -14,126 +14,120 @@ namespace {
 
 kiln_stream_t ks(hipStream_t s) { return (kiln_stream_t)s; }
 
-// ModelSamplingDiscreteFlow(shift): sigma(t) = shift t / (1 + (shift - 1) t); the 1000-entry table holds
-// sigma((i + 1) / 1000) in float32 (pipeline.cu:66-78, 100-107).
-double shifted(double shift, double t) { return shift == 1.0 ? t : shift * t / (1.0 + (shift - 1.0) * t); }
+// Flow-space model sampling (ComfyUI's ModelSamplingDiscreteFlow with shift s): sigma(t) = s t / (1 + (s - 1) t),
+// and the model's discrete table holds sigma((i + 1) / 1000) in float32 (pipeline.cu:66-78, 100-107). A flow
+// model's timestep is its sigma, so the schedulers that work in timestep space apply only the shift.
+struct FlowSpace {
+    double shift;
+    std::vector<float> table;  // ascending: table[0] = sigma_min, table[999] = sigma_max
 
-std::vector<float> sigma_table(float shift) {
-    std::vector<float> tab(1000);
-    for (int i = 0; i < 1000; i++) {
-        const float t = (float)(i + 1) / 1000.f;
-        tab[i] = shift == 1.f ? t : shift * t / (1.f + (shift - 1.f) * t);
+    explicit FlowSpace(float s) : shift(s), table(1000) {
+        for (int i = 0; i < 1000; i++) {
+            const float t = (float)(i + 1) / 1000.f;
+            table[i] = s == 1.f ? t : s * t / (1.f + (s - 1.f) * t);
+        }
     }
-    return tab;
-}
+    double lo() const { return table.front(); }
+    double hi() const { return table.back(); }
+    double sigma(double t) const { return shift == 1.0 ? t : shift * t / (1.0 + (shift - 1.0) * t); }
+};
 
-// Each scheduler returns its whole schedule of `steps` steps (steps + 1 sigmas, or fewer where the scheduler
-// merges duplicates), ending in 0. smin / smax are the table's ends; in flow space timestep(sigma) = sigma.
+// Schedules have `steps` steps (steps + 1 sigmas, or fewer where a scheduler drops repeats) and end in 0.
 using Schedule = std::vector<float>;
 
-Schedule sched_simple(int steps, const std::vector<float>& tab) {
+// The fraction k / (n - 1) of n evenly spaced points (the single point of n = 1 sits at 0).
+double frac(int k, int n) { return n == 1 ? 0.0 : (double)k / (n - 1); }
+
+// Schedulers that space the steps evenly in a warped coordinate w(sigma) between w(sigma_max) and w(sigma_min)
+// and map back: karras (w = sigma^(1/7), Karras et al. 2022, eq. 5), exponential (w = log sigma) and
+// kl_optimal (w = atan sigma, Sabour et al. 2024).
+template <class W, class Winv>
+Schedule warped(const FlowSpace& fs, int steps, W w, Winv winv) {
+    const double top = w(fs.hi()), bottom = w(fs.lo());
+    Schedule s(steps + 1, 0.f);
+    for (int k = 0; k < steps; k++) s[k] = (float)winv(top + frac(k, steps) * (bottom - top));
+    return s;
+}
+
+// Schedulers that space timesteps evenly: normal (steps points from sigma_max to sigma_min; if the last
+// one maps to 0 it becomes an extra step instead of the appended 0) and sgm_uniform (steps + 1 points, the last
+// replaced by 0). ComfyUI's normal_scheduler.
+Schedule timestep_uniform(const FlowSpace& fs, int steps, bool sgm) {
+    const double t0 = fs.hi(), t1 = fs.lo();
+    const bool extra = !sgm && std::fabs(fs.sigma(t1)) < 1e-5;
+    const int n = extra ? steps + 1 : steps;
     Schedule s;
+    for (int k = 0; k < n; k++) {
+        const double u = sgm ? (double)k / steps : frac(k, n);
+        s.push_back((float)fs.sigma(t0 + u * (t1 - t0)));
+    }
+    if (!extra) s.push_back(0.f);
+    return s;
+}
+
+// Schedulers that pick entries of the model's table by index (ComfyUI's simple, ddim_uniform and beta
+// schedulers). Repeated indices are dropped where the scheduler asks for it.
+Schedule from_table(const FlowSpace& fs, const std::vector<int>& idx, bool drop_repeats) {
+    Schedule s;
+    for (size_t k = 0; k < idx.size(); k++)
+        if (!drop_repeats || k == 0 || idx[k] != idx[k - 1]) s.push_back(fs.table[idx[k]]);
+    s.push_back(0.f);
+    return s;
+}
+
+std::vector<int> idx_simple(int steps) {  // every 1000/steps-th entry from the top
+    std::vector<int> idx(steps);
     const double stride = 1000.0 / steps;
-    for (int k = 0; k < steps; k++) s.push_back(tab[999 - (int)(k * stride)]);
-    s.push_back(0.f);
-    return s;
+    for (int k = 0; k < steps; k++) idx[k] = 999 - (int)(k * stride);
+    return idx;
 }
 
-// linspace in timestep space between smax and smin, mapped back through the shift
-Schedule sched_uniform_t(int steps, double shift, double smin, double smax, bool sgm) {
+std::vector<int> idx_beta(int steps) {  // the Beta(0.6, 0.6) quantiles of 1 - k/steps, rounded to the table
+    std::vector<int> idx(steps);
+    for (int k = 0; k < steps; k++) idx[k] = (int)std::nearbyint(beta_quantile(1.0 - (double)k / steps, 0.6, 0.6) * 999.0);
+    return idx;
+}
+
+// ddim_uniform: entries 1, 1 + c, 1 + 2c, ... (c = 1000 / steps) from the bottom of the table, reversed, after a 0
+// unless entry 1 is itself ~0 (then one more step). The 0 comes first in ascending order, so it ends the schedule.
+Schedule ddim_uniform(const FlowSpace& fs, int steps) {
+    const bool zero_at_1 = std::fabs(fs.table[1]) < 1e-5;
+    const int c = std::max(1000 / (zero_at_1 ? steps + 1 : steps), 1);
     Schedule s;
-    if (sgm) {  // steps + 1 points, the last dropped, then 0
-        for (int k = 0; k < steps; k++) s.push_back((float)shifted(shift, smax + (smin - smax) * k / steps));
-        s.push_back(0.f);
-        return s;
-    }
-    int n = steps;
-    const bool ends_at_zero = std::fabs(shifted(shift, smin)) < 1e-5;
-    if (ends_at_zero) n++;
-    for (int k = 0; k < n; k++) s.push_back((float)shifted(shift, n == 1 ? smax : smax + (smin - smax) * k / (n - 1)));
-    if (!ends_at_zero) s.push_back(0.f);
+    for (int x = 1; x < 1000; x += c) s.push_back(fs.table[x]);
+    std::reverse(s.begin(), s.end());
+    if (!zero_at_1) s.push_back(0.f);
     return s;
 }
 
-Schedule sched_karras(int steps, double smin, double smax) {
-    const double rho = 7.0, hi = std::pow(smax, 1.0 / rho), lo = std::pow(smin, 1.0 / rho);
-    Schedule s;
-    for (int k = 0; k < steps; k++) {
-        const double f = steps == 1 ? 0.0 : (double)k / (steps - 1);
-        s.push_back((float)std::pow(hi + f * (lo - hi), rho));
-    }
-    s.push_back(0.f);
-    return s;
-}
-
-Schedule sched_exponential(int steps, double smin, double smax) {
-    const double lhi = std::log(smax), llo = std::log(smin);
-    Schedule s;
-    for (int k = 0; k < steps; k++) s.push_back((float)std::exp(steps == 1 ? lhi : lhi + (llo - lhi) * k / (steps - 1)));
-    s.push_back(0.f);
-    return s;
-}
-
-Schedule sched_ddim_uniform(int steps, const std::vector<float>& tab) {
-    Schedule up;  // ascending, then reversed
-    int n = steps;
-    if (std::fabs(tab[1]) < 1e-5) n++;
-    else up.push_back(0.f);
-    const int stride = std::max(1000 / n, 1);
-    for (int x = 1; x < 1000; x += stride) up.push_back(tab[x]);
-    return Schedule(up.rbegin(), up.rend());
-}
-
-Schedule sched_beta(int steps, const std::vector<float>& tab) {
-    Schedule s;
-    int prev = -1;
-    for (int k = 0; k < steps; k++) {
-        const int t = (int)std::nearbyint(beta_quantile(1.0 - (double)k / steps, 0.6, 0.6) * 999.0);
-        if (t != prev) s.push_back(tab[t]);
-        prev = t;
-    }
-    s.push_back(0.f);
-    return s;
-}
-
-Schedule sched_linear_quadratic(int steps, double smax) {
+// linear_quadratic (ComfyUI, from Movie Gen): the noise level nu rises linearly to 0.025 over the first half of
+// the steps, then along the quadratic that meets it there and reaches 1 at the end; sigma = (1 - nu) sigma_max.
+Schedule linear_quadratic(const FlowSpace& fs, int steps) {
     if (steps == 1) return {1.f, 0.f};
-    const double thr = 0.025;
-    const int lin = steps / 2, quad = steps - lin;
-    const double diff = lin - thr * steps;
-    const double qa = diff / (lin * (double)quad * quad), qb = thr / lin - 2 * diff / ((double)quad * quad),
-                 qc = qa * lin * lin;
-    Schedule s;
-    auto put = [&](double v) { s.push_back((float)((1.0 - v) * smax)); };
-    for (int k = 0; k < lin; k++) put(k * thr / lin);
-    for (int k = lin; k < steps; k++) put(qa * k * k + qb * k + qc);
-    put(1.0);
-    return s;
-}
-
-Schedule sched_kl_optimal(int steps, double smin, double smax) {
-    Schedule s;
-    const double amin = std::atan(smin), amax = std::atan(smax);
-    for (int k = 0; k < steps; k++) {
-        const double f = steps == 1 ? 0.0 : (double)k / (steps - 1);
-        s.push_back((float)std::tan(f * amin + (1 - f) * amax));
-    }
-    s.push_back(0.f);
+    const double th = 0.025;
+    const int nl = steps / 2, nq = steps - nl;
+    const double excess = nl - th * steps;  // what the quadratic part must add above a straight continuation
+    const double q2 = excess / (nl * (double)nq * nq), q1 = th / nl - 2 * excess / ((double)nq * nq), q0 = q2 * nl * nl;
+    auto nu = [&](int k) { return k < nl ? k * th / nl : q2 * k * k + q1 * k + q0; };
+    Schedule s(steps + 1);
+    for (int k = 0; k < steps; k++) s[k] = (float)((1.0 - nu(k)) * fs.hi());
+    s[steps] = 0.f;  // nu = 1
     return s;
 }
 
 Schedule full_schedule(const std::string& name, int steps, float shift) {
-    const std::vector<float> tab = sigma_table(shift);
-    const double smin = tab[0], smax = tab[999];
-    if (name == "simple") return sched_simple(steps, tab);
-    if (name == "normal") return sched_uniform_t(steps, shift, smin, smax, false);
-    if (name == "sgm_uniform") return sched_uniform_t(steps, shift, smin, smax, true);
-    if (name == "karras") return sched_karras(steps, smin, smax);
-    if (name == "exponential") return sched_exponential(steps, smin, smax);
-    if (name == "ddim_uniform") return sched_ddim_uniform(steps, tab);
-    if (name == "beta") return sched_beta(steps, tab);
-    if (name == "linear_quadratic") return sched_linear_quadratic(steps, smax);
-    if (name == "kl_optimal") return sched_kl_optimal(steps, smin, smax);
+    const FlowSpace fs(shift);
+    if (name == "simple") return from_table(fs, idx_simple(steps), false);
+    if (name == "beta") return from_table(fs, idx_beta(steps), true);
+    if (name == "ddim_uniform") return ddim_uniform(fs, steps);
+    if (name == "normal" || name == "sgm_uniform") return timestep_uniform(fs, steps, name == "sgm_uniform");
+    if (name == "karras")
+        return warped(fs, steps, [](double v) { return std::pow(v, 1.0 / 7.0); }, [](double w) { return std::pow(w, 7.0); });
+    if (name == "exponential")
+        return warped(fs, steps, [](double v) { return std::log(v); }, [](double w) { return std::exp(w); });
+    if (name == "kl_optimal")
+        return warped(fs, steps, [](double v) { return std::atan(v); }, [](double w) { return std::tan(w); });
+    if (name == "linear_quadratic") return linear_quadratic(fs, steps);
     throw std::runtime_error("unknown scheduler " + name);
 }
 
@@ -154,7 +148,7 @@ std::vector<float> flow_sigmas(int steps, float shift, float denoise) {
     if (denoise <= 0.f) return {};
     const int total = partial(denoise) ? partial_total(steps, denoise) : steps;
     if (total < steps) throw std::runtime_error("flow_sigmas: denoise must be in (0, 1]");
-    return tail(sched_simple(total, sigma_table(shift)), steps);
+    return tail(full_schedule("simple", total, shift), steps);
 }
 
 std::vector<float> schedule_sigmas(const std::string& name, int steps, float shift, float denoise) {
@@ -223,51 +217,78 @@ double beta_quantile(double p, double a, double b) {
     return 0.5 * (lo + hi);
 }
 
-StepCoef step_coef(const std::string& sampler, const std::vector<float>& sig, int i, bool have_old) {
-    const double s = sig[i], sn = sig[i + 1];
-    if (sampler == "euler" || !have_old || sn == 0.0) return {(float)(sn / s), (float)(1.0 - sn / s), 0.f};
-    // log-sigma time t = -log sigma, step h = t_{i+1} - t_i (ComfyUI's k-diffusion, deterministic variants)
-    const double t = -std::log(s), tn = -std::log(sn), tp = -std::log((double)sig[i - 1]), h = tn - t;
+namespace {
+// phi_1(z) = (e^z - 1) / z and phi_2(z) = (phi_1(z) - 1) / z, the weights of exponential integrators.
+double phi1(double z) { return std::expm1(z) / z; }
+double phi2(double z) { return (phi1(z) - 1.0) / z; }
+}  // namespace
+
+// The deterministic samplers in exponential-integrator form (ComfyUI's sample_euler, sample_dpmpp_2m and
+// sample_res_multistep with eta 0, in the data-prediction parameterization of Lu et al., DPM-Solver++): with the
+// log-sigma time lambda = -log sigma and the step h = lambda_{i+1} - lambda_i, the latent keeps the share
+// e^-h = sigma_{i+1} / sigma_i and the remaining 1 - e^-h = h phi_1(-h) goes to a combination of the current and
+// the previous data estimates, which the second-order methods extrapolate over the previous step h_prev.
+LinearStep linear_step(const std::string& sampler, const std::vector<float>& sig, int i, bool have_old) {
+    const double s_now = sig[i], s_next = sig[i + 1];
+    LinearStep w{(float)(s_next / s_now), (float)(1.0 - s_next / s_now), 0.f};  // first order: Euler = DDIM
+    if (sampler == "euler" || !have_old || s_next == 0.0) return w;
+    const double lam = -std::log(s_now), lam_next = -std::log(s_next), lam_prev = -std::log((double)sig[i - 1]);
+    const double h = lam_next - lam, h_prev = lam - lam_prev;
     if (sampler == "dpmpp_2m") {
-        const double r = (t - tp) / h, em = -std::expm1(-h);
-        return {(float)(sn / s), (float)(em * (1.0 + 1.0 / (2.0 * r))), (float)(-em / (2.0 * r))};
+        // data estimate extrapolated to the middle of the step: (1 + 1/2r) den - 1/2r old, r = h_prev / h
+        const double share = -std::expm1(-h), half_inv_r = h / (2.0 * h_prev);
+        w.den_w = (float)(share * (1.0 + half_inv_r));
+        w.old_w = (float)(-share * half_inv_r);
+        return w;
     }
-    // res_multistep with eta 0: phi functions of -h, c2 = (t_prev - t) / h
-    const double c2 = (tp - t) / h, phi1 = std::expm1(-h) / (-h), phi2 = (phi1 - 1.0) / (-h);
-    return {(float)std::exp(-h), (float)(h * (phi1 - phi2 / c2)), (float)(h * (phi2 / c2))};
+    // res_multistep: second-order Adams-type weights through the previous node at c = -h_prev / h
+    const double c = -h_prev / h, p1 = phi1(-h), p2 = phi2(-h);
+    w.x_w = (float)std::exp(-h);
+    w.den_w = (float)(h * (p1 - p2 / c));
+    w.old_w = (float)(h * (p2 / c));
+    return w;
 }
 
-ErSdeCoef ersde_coef(const std::vector<float>& sig, int i) {
-    // lambda = sigma / (1 - sigma), alpha = 1 - sigma, noise scaler f(l) = l (exp(l^0.3) + 10)
-    auto lam = [&](int k) { const double v = sig[k]; return v / (1.0 - v); };
+namespace {
+// The left Riemann sum of g over [lo, hi] with n points (ComfyUI's er_sde integrates with 200 of them).
+template <class G>
+double left_sum(G g, double lo, double hi, int n) {
+    const double dx = (hi - lo) / n;
+    double acc = 0.0;
+    for (int k = 0; k < n; k++) acc += g(lo + k * dx);
+    return acc * dx;
+}
+}  // namespace
+
+// er_sde (Cui et al. 2025, "Elucidating the solution space of extended reverse-time SDEs"; ComfyUI's
+// sample_er_sde with max_stage 3 and its default noise scaler), for a flow model: the SDE runs in
+// lambda = sigma / alpha with alpha = 1 - sigma, and the noise scaler is f(lambda) = lambda (e^(lambda^0.3) + 10).
+// From lambda_i to lambda_{i+1} = lambda_i + dl:
+//   x' = (alpha'/alpha) r x + alpha' (1 - r) den                                    r = f(lambda') / f(lambda)
+//      + alpha' (dl + f(lambda') int 1/f) D1                   from the 2nd step,  D1 = (den - old) / (lambda - lambda_{i-1})
+//      + alpha' (dl^2 / 2 + f(lambda') int (l - lambda)/f) D2  from the 3rd step,  D2 = (D1 - D1_prev) 2 / (lambda - lambda_{i-2})
+//      + alpha' sqrt(lambda'^2 - lambda^2 r^2) noise
+// with both integrals over [lambda', lambda].
+ErSdeStep ersde_step(const std::vector<float>& sig, int i) {
+    auto lambda = [&](int k) { return (double)sig[k] / (1.0 - (double)sig[k]); };
     auto f = [](double l) { return l * (std::exp(std::pow(l, 0.3)) + 10.0); };
-    const double ls = lam(i), lt = lam(i + 1);
-    const double al_s = sig[i] / ls, al_t = sig[i + 1] / lt;
-    const double r = f(lt) / f(ls);
-    ErSdeCoef c{};
-    c.stage = std::min(3, i + 1);
-    c.a = (float)(al_t / al_s * r);
-    c.b = (float)(al_t * (1.0 - r));
-    if (c.stage >= 2) {
-        // integrals of 1/f and (l - l_i)/f over [l_{i+1}, l_i]: 200-point left sums from l_{i+1}
-        const double dl = lt - ls, h = -dl / 200.0;
-        double s1 = 0.0, s2 = 0.0;
-        for (int k = 0; k < 200; k++) {
-            const double l = lt + k * h, fl = f(l);
-            s1 += 1.0 / fl;
-            s2 += (l - ls) / fl;
-        }
-        s1 *= h;
-        s2 *= h;
-        c.c2 = (float)(al_t * (dl + s1 * f(lt)));
-        c.inv2 = (float)(1.0 / (ls - lam(i - 1)));
-        if (c.stage >= 3) {
-            c.c3 = (float)(al_t * (dl * dl / 2.0 + s2 * f(lt)));
-            c.inv3 = (float)(2.0 / (ls - lam(i - 2)));
-        }
-    }
-    c.cn = (float)(al_t * std::sqrt(std::max(0.0, lt * lt - ls * ls * r * r)));
-    return c;
+    const double l_now = lambda(i), l_next = lambda(i + 1), dl = l_next - l_now;
+    const double alpha_now = sig[i] / l_now, alpha_next = sig[i + 1] / l_next;  // = 1 - sigma, as ComfyUI forms it
+    const double r = f(l_next) / f(l_now);
+    ErSdeStep e{};
+    e.order = std::min(3, i + 1);
+    e.x_w = (float)(alpha_next / alpha_now * r);
+    e.den_w = (float)(alpha_next * (1.0 - r));
+    e.noise_w = (float)(alpha_next * std::sqrt(std::max(0.0, l_next * l_next - l_now * l_now * r * r)));
+    if (e.order < 2) return e;
+    const double i1 = left_sum([&](double l) { return 1.0 / f(l); }, l_next, l_now, 200);
+    e.d1_w = (float)(alpha_next * (dl + i1 * f(l_next)));
+    e.d1_inv = (float)(1.0 / (l_now - lambda(i - 1)));
+    if (e.order < 3) return e;
+    const double i2 = left_sum([&](double l) { return (l - l_now) / f(l); }, l_next, l_now, 200);
+    e.d2_w = (float)(alpha_next * (dl * dl / 2.0 + i2 * f(l_next)));
+    e.d2_inv = (float)(2.0 / (l_now - lambda(i - 2)));
+    return e;
 }
 
 // ---- sample() ----
@@ -331,7 +352,7 @@ SampleResult sample(VelocityModel& model, float* x, int Hl, int Wl, bool negativ
         const bool cfg_now = negative && i < cfg_steps;
         bool skipped = false;
         float* outs[2] = {v, vn};
-        model.forward(outs, xin, s * sp.timestep_mult, cfg_now, allow, &skipped);
+        model.forward(outs, xin, s, s * sp.timestep_mult, cfg_now, allow, &skipped);
         if (cfg_now) ck(kiln_cfg_combine(v, vn, sp.cfg, n, st), "cfg_combine");
         if (use_cache) {
             if (skipped) res.cache_skips++, run++;
@@ -364,17 +385,17 @@ SampleResult sample(VelocityModel& model, float* x, int Hl, int Wl, bool negativ
             if (sn == 0.f) {
                 ck(kiln_flow_update(x, den, nullptr, 0.f, 1.f, 0.f, n, st), "final step");
             } else {
-                const ErSdeCoef c = ersde_coef(sig, i);
+                const ErSdeStep e = ersde_step(sig, i);
                 ck(kiln_torch_randn(nz.data(), sp.seed + 1 + i, n), "torch_randn");
                 ck_hip(hipMemcpyAsync(anoise, nz.data(), n * 4, hipMemcpyHostToDevice, stream), "noise upload");
-                ck(kiln_flow_ersde_step(x, den, old, oldd, anoise, c.a, c.b, c.c2, c.inv2, c.c3, c.inv3, c.cn, c.stage,
+                ck(kiln_flow_ersde_step(x, den, old, oldd, anoise, e.x_w, e.den_w, e.d1_w, e.d1_inv, e.d2_w, e.d2_inv, e.noise_w, e.order,
                                         n, st),
                    "er_sde step");
                 ck_hip(hipStreamSynchronize(stream), "noise upload");
             }
         } else {
-            const StepCoef co = step_coef(sp.sampler, sig, i, have_old);
-            ck(kiln_flow_update(x, den, have_old ? old : nullptr, co.a, co.b, co.c, n, st), "sampler step");
+            const LinearStep w = linear_step(sp.sampler, sig, i, have_old);
+            ck(kiln_flow_update(x, den, have_old ? old : nullptr, w.x_w, w.den_w, w.old_w, n, st), "sampler step");
         }
         std::swap(den, old);
         have_old = true;
@@ -395,10 +416,10 @@ DitVelocity::DitVelocity(Dit& dit, int Hl, int Wl, const CachedContext* pos, con
     sc_.threshold = cache_threshold;
 }
 
-void DitVelocity::forward(float* const* outs, const float* x, float t, bool cfg_now, bool cache_allow,
+void DitVelocity::forward(float* const* outs, const float* x, float sigma, float t, bool cfg_now, bool cache_allow,
                           bool* cache_skipped) {
     NagParams nag = nag_;
-    if (nag.neg && t / tmult_ < nag_end_) nag.neg = nullptr;  // NAG only while sigma >= nag_sigma_end
+    if (nag.neg && !(sigma >= nag_end_)) nag.neg = nullptr;  // NAG only while sigma >= nag_sigma_end
     sc_.allow = cache_allow;
     StepCache* sc = sc_.threshold > 0.f ? &sc_ : nullptr;
     if (cfg_now && batch_) {

@@ -24,26 +24,29 @@ bool known_sampler(const std::string& name);
 double beta_quantile(double p, double a, double b);
 double beta_cdf(double x, double a, double b);
 
-// x <- a x + b den + c old from sigma_i to sigma_{i+1} (pipeline.cu:396-411)
-struct StepCoef {
-    float a, b, c;
+// One deterministic step from sigma_i to sigma_{i+1}: x <- x_w x + den_w den + old_w old (the samplers of
+// pipeline.cu:396-411)
+struct LinearStep {
+    float x_w, den_w, old_w;
 };
-StepCoef step_coef(const std::string& sampler, const std::vector<float>& sig, int i, bool have_old);
+LinearStep linear_step(const std::string& sampler, const std::vector<float>& sig, int i, bool have_old);
 
-// er_sde (pipeline.cu:361-391)
-struct ErSdeCoef {
-    float a, b, c2, inv2, c3, inv3, cn;
-    int stage;
+// One er_sde step (pipeline.cu:361-391): x <- x_w x + den_w den + d1_w D1 + d2_w D2 + noise_w noise, with
+// D1 = (den - old) d1_inv and D2 = (D1 - D1_prev) d2_inv; `order` terms are active (1: the first two).
+struct ErSdeStep {
+    float x_w, den_w, d1_w, d1_inv, d2_w, d2_inv, noise_w;
+    int order;
 };
-ErSdeCoef ersde_coef(const std::vector<float>& sig, int i);
+ErSdeStep ersde_step(const std::vector<float>& sig, int i);
 
 // The velocity model the sampler drives. forward() writes the prompt's velocity into outs[0] and, when cfg_now,
-// the negative context's into outs[1], for the latent x at timestep t. cache_allow tells a model with a step
+// the negative context's into outs[1], for the latent x at noise level sigma, whose model timestep is t (sigma times
+// the model's timestep multiplier). cache_allow tells a model with a step
 // cache whether it may skip this step; it reports a skip through *cache_skipped.
 class VelocityModel {
    public:
     virtual ~VelocityModel() = default;
-    virtual void forward(float* const* outs, const float* x, float t, bool cfg_now, bool cache_allow,
+    virtual void forward(float* const* outs, const float* x, float sigma, float t, bool cfg_now, bool cache_allow,
                          bool* cache_skipped) = 0;
 };
 
@@ -87,10 +90,8 @@ class DitVelocity : public VelocityModel {
    public:
     DitVelocity(Dit& dit, int Hl, int Wl, const CachedContext* pos, const CachedContext* neg, const NagParams& nag,
                 float nag_sigma_end, float cache_threshold, bool batch, bool fp32);
-    void forward(float* const* outs, const float* x, float t, bool cfg_now, bool cache_allow,
+    void forward(float* const* outs, const float* x, float sigma, float t, bool cfg_now, bool cache_allow,
                  bool* cache_skipped) override;
-    // the sigma of the step about to run (NAG's cut-off), set by the sampler through the timestep
-    void set_timestep_mult(float m) { tmult_ = m; }
 
    private:
     Dit& dit_;
@@ -100,7 +101,6 @@ class DitVelocity : public VelocityModel {
     float nag_end_;
     StepCache sc_;
     bool batch_, fp32_;
-    float tmult_ = 1.f;
 };
 
 }  // namespace kiln

@@ -95,6 +95,24 @@ def test_argument_checks_return_before_any_gpu_call():
     assert L.kiln_step_coef(b"euler", sig, 2, 0, 0, abc) == 0 and abs(abc[0]) < 1e-12 and abs(abc[1] - 1) < 1e-7
 
 
+def test_device_failures_keep_their_status():
+    """A HIP failure inside the driver comes back as KILN_EHIP, not as a bad argument: on a machine without a GPU
+    caching a context fails in its first hipMalloc (the C ABI maps the driver's typed errors to their status)."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("needs a machine without a GPU")
+    L = dit.dlib()
+    out = ctypes.c_void_p()
+    assert L.kiln_dit_create(ctypes.byref(dit.Dims(2, 4, 1024, 512, 1e-6)), None, ctypes.byref(out)) == 0
+    try:
+        buf = (ctypes.c_float * 4096)()
+        ctx = ctypes.c_void_p()
+        assert L.kiln_dit_cache_context(out, buf, 1, 1, 0, ctypes.byref(ctx)) == kiln_amd.KILN_EHIP
+        assert b"hipMalloc" in L.kiln_dit_last_error()
+    finally:
+        L.kiln_dit_destroy(out)
+
+
 def test_engine_reports_fatal_without_a_device():
     """kiln_engine's start-up failure path (main.cpp:647-660: a fatal event, exit code 1), on a machine without
     a GPU; the protocol itself is tested on the GPU (tests/test_engine_protocol_gpu.py)."""

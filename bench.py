@@ -232,8 +232,9 @@ def linear16_cases(torch, kiln_amd, tm, dev, steps, warmup):
 
 
 def cpu_model():
-    """The host CPU as /proc/cpuinfo names it (lscpu's "Model name"), with its family and model numbers: a
-    virtualized host may report only "AMD EPYC", and the family (26 = Zen 5, 25 = Zen 3/4) still dates it."""
+    """The host CPU as /proc/cpuinfo names it (lscpu's "Model name"), with its family and model numbers, and the
+    firmware's name for it where lscpu reports one ("BIOS Model name": a virtualized host may show only
+    "AMD EPYC" in /proc/cpuinfo)."""
     info = {}
     try:
         with open("/proc/cpuinfo") as f:
@@ -249,7 +250,17 @@ def cpu_model():
     if "model name" not in info:
         return None
     extra = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model") if k in info)
-    return f"{info['model name']} ({extra})" if extra else info["model name"]
+    name = f"{info['model name']} ({extra})" if extra else info["model name"]
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for ln in out.splitlines():
+            k, _, v = ln.partition(":")
+            if k.strip() == "BIOS Model name" and v.strip() and v.strip() != info["model name"]:
+                name += f"; BIOS: {v.strip()}"
+    except (OSError, ValueError, __import__("subprocess").SubprocessError):
+        pass
+    return name
 
 
 def cpu_baseline(case, target_s=10.0):
@@ -287,6 +298,82 @@ def cpu_baseline(case, target_s=10.0):
                 nproc=os.cpu_count(), cpu_model=cpu_model(),
                 sample=f"{what} x {H} heads x {T} keys (+ QK-RMSNorm, RoPE), fp32 two-pass reference attention, "
                        f"{dt:.1f} s")
+
+
+def cpu_baseline_configs():
+    """The same CPU reference (the fp32 two-pass attention of bench/flash_test.cu:10-32 with the QK-RMSNorm and
+    RoPE passes and the NAG combine of engine/src/dit.cu:295-324, all from oracle/oracle.c) on configs 1-3 in
+    full and on one of config 5's 28 blocks (its self-attention of the CFG pair, the cross-attention of both
+    items and the NAG negative attention of item 0 over L = 512, and the NAG combine), scaled by 28 to a step.
+    Inputs are seeded N(0,1) rows of each config's shapes (the CPU time does not depend on the values); Q/K
+    norm weights 1 (torch's RMSNorm init)."""
+    import numpy as np
+    import oracle
+    rng = np.random.default_rng(7)
+
+    def randn(*shape):
+        return rng.standard_normal(shape, dtype=np.float32)
+
+    w1 = np.full(D, 0x3F80, np.uint16)  # bf16 1.0
+
+    def normed_roped(x, c, s):
+        return oracle.rope_half(oracle.rmsnorm_rows(x, w1).reshape(x.shape[0], H * D), H, c, s)
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    out = {}
+    # config 1: plain self-attention, S = 1536, B = 1
+    q, k, v = randn(1536, H * D), randn(1536, H * D), randn(1536, H * D)
+    dt = timed(lambda: oracle.ref_attn_f32(q, k, v, H))
+    fl = 4.0 * H * 1536 * 1536 * D
+    out["config1"] = dict(tflops=round(fl / dt / 1e12, 5), seconds=round(dt, 3),
+                          sample="in full: B=1, S=1536, 16 heads, fp32 two-pass reference attention")
+    # config 2: the CFG pair at T = 1536 with QK-RMSNorm and RoPE
+    c2, s2 = (t.numpy() for t in __import__("kiln_amd").cosmos_rope_tables(32, 48))
+    qs, ks, vs = ([randn(1536, H * D) for _ in range(2)] for _ in range(3))
+    dt = timed(lambda: [oracle.ref_attn_f32(normed_roped(qs[b], c2, s2), normed_roped(ks[b], c2, s2), vs[b], H)
+                        for b in range(2)])
+    fl = 2 * 4.0 * H * 1536 * 1536 * D
+    out["config2"] = dict(tflops=round(fl / dt / 1e12, 5), seconds=round(dt, 3),
+                          sample="in full: B=2, T=1536, 16 heads, QK-RMSNorm + RoPE + fp32 two-pass attention")
+    # config 3: cross-attention over a positive and a negative context of 512 keys, NAG combine
+    q3 = oracle.rmsnorm_rows(randn(1536, H * D), w1).reshape(1536, H * D)
+    kp, vp, kn, vn = (randn(512, H * D) for _ in range(4))
+
+    def cfg3():
+        zp = oracle.ref_attn_f32(q3, kp, vp, H)
+        zn = oracle.ref_attn_f32(q3, kn, vn, H)
+        oracle.nag(zp, zn)
+
+    dt = timed(cfg3)
+    fl = 2 * 4.0 * H * 1536 * 512 * D
+    out["config3"] = dict(tflops=round(fl / dt / 1e12, 5), seconds=round(dt, 3),
+                          sample="in full: 1536 queries x (positive + negative) 512-key contexts, 16 heads, NAG")
+    # config 5: one block of 28 (T = 3456, B = 2, L = 512), scaled to the step
+    T5, L5 = 3456, 512
+    c5, s5 = (t.numpy() for t in __import__("kiln_amd").cosmos_rope_tables(48, 72))
+    qs, ks, vs, qc = ([randn(T5, H * D) for _ in range(2)] for _ in range(4))
+    ctx = [(randn(L5, H * D), randn(L5, H * D)) for _ in range(3)]
+
+    def block():
+        for b in range(2):
+            oracle.ref_attn_f32(normed_roped(qs[b], c5, s5), normed_roped(ks[b], c5, s5), vs[b], H)
+        qn = [oracle.rmsnorm_rows(qc[b], w1).reshape(T5, H * D) for b in range(2)]
+        z0 = oracle.ref_attn_f32(qn[0], *ctx[0], H)
+        oracle.ref_attn_f32(qn[1], *ctx[1], H)
+        zn = oracle.ref_attn_f32(qn[0], *ctx[2], H)
+        oracle.nag(z0, zn)
+
+    dt = timed(block)
+    fl = 4.0 * 2 * H * T5 * T5 * D + 4.0 * 3 * H * T5 * L5 * D
+    out["config5"] = dict(tflops=round(fl / dt / 1e12, 5), ms_per_step=round(28 * dt * 1e3, 1), seconds=round(dt, 3),
+                          sample="block 0 of 28 in full (self-attention of the CFG pair with QK-RMSNorm + RoPE, "
+                                 "cross-attention of both items and the NAG negative over 512 keys, NAG combine), "
+                                 "x 28 for the step")
+    return out
 
 
 def main():
@@ -486,6 +573,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg4)
+        cpu["configs"] = cpu_baseline_configs()
         log(f"cpu baseline: {cpu}")
 
     line = {

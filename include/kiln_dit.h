@@ -71,6 +71,11 @@ int kiln_dit_set_block(kiln_dit* dit, int i, const kiln_dit_block_weights* w);
  * attention as npad zero keys). fp32 != 0 also keeps fp32 K/V for the fp32 path. */
 int kiln_dit_cache_context(kiln_dit* dit, const float* ctx, int real, int len, int fp32, kiln_dit_context** out);
 void kiln_dit_context_destroy(kiln_dit_context* c);
+/* The prepared K/V of block `block` of a cached context (the layout kiln_kv_prepare writes, `real` keys, the
+ * other len - real rows as npad zero keys): what Dit::forward_batch hands kiln_cross_attn_nag /
+ * kiln_dit_cross_attn_x16, for callers that drive a block's cross-attention themselves (Dit::kv_for,
+ * engine/src/dit.cu:407-413). The pointer lives as long as the context. */
+int kiln_dit_context_kv(const kiln_dit_context* c, int block, const uint16_t** kvp, int* real, int* len);
 
 int kiln_dit_step_cache_create(float threshold, kiln_dit_step_cache** out);
 void kiln_dit_step_cache_destroy(kiln_dit_step_cache* sc);

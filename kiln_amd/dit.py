@@ -59,6 +59,7 @@ _SIGS = {
     "kiln_dit_set_block": (_i, [_vp, _i, ctypes.POINTER(BlockWeights)]),
     "kiln_dit_cache_context": (_i, [_vp, _vp, _i, _i, _i, ctypes.POINTER(_vp)]),
     "kiln_dit_context_destroy": (None, [_vp]),
+    "kiln_dit_context_kv": (_i, [_vp, _i, ctypes.POINTER(_vp), ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "kiln_dit_step_cache_create": (_i, [_f, ctypes.POINTER(_vp)]),
     "kiln_dit_step_cache_destroy": (None, [_vp]),
     "kiln_dit_step_cache_set_allow": (_i, [_vp, _i]),
@@ -125,6 +126,16 @@ def _f32(t, n=None, name=""):
     return _p(t)
 
 
+class _DevPtr:
+    """A device address owned by another object (kept alive with it), with torch's data_ptr() spelling."""
+
+    def __init__(self, addr, owner):
+        self._addr, self._owner = addr, owner
+
+    def data_ptr(self):
+        return self._addr
+
+
 class Context:
     """A text context cached for one generation (Dit::cache_context): real rows and the padded length."""
 
@@ -134,6 +145,14 @@ class Context:
     @property
     def handle(self):
         return self._h
+
+    def kv(self, block):
+        """Block `block`'s prepared K/V (kiln_dit_context_kv): an object with data_ptr(), as the cross-attention
+        entry points of kiln_amd take prepared buffers; valid while this context lives."""
+        p, real, length = ctypes.c_void_p(), ctypes.c_int(), ctypes.c_int()
+        _check(dlib().kiln_dit_context_kv(self._h, int(block), ctypes.byref(p), ctypes.byref(real),
+                                          ctypes.byref(length)))
+        return _DevPtr(p.value, self)
 
     def __del__(self):
         if getattr(self, "_h", None):

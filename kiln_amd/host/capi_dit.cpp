@@ -170,6 +170,19 @@ int kiln_dit_cache_context(kiln_dit* dit, const float* ctx, int real, int len, i
 
 void kiln_dit_context_destroy(kiln_dit_context* c) { delete c; }
 
+int kiln_dit_context_kv(const kiln_dit_context* c, int block, const uint16_t** kvp, int* real, int* len) {
+    if (!c || !c->c || !kvp || !real || !len) return fail(KILN_EINVAL, "context_kv: null argument");
+    const kiln::CachedContext& cc = *c->c;
+    const size_t blocks = cc.kv_per_block ? cc.kv16.bytes() / cc.kv_per_block : 0;
+    if (block < 0 || (size_t)block >= blocks) 
+        return fail(KILN_EINVAL, "context_kv: block " + std::to_string(block) + " outside the context's " +
+                                     std::to_string(blocks) + " blocks");
+    *kvp = cc.kv(block);
+    *real = cc.real;
+    *len = cc.len;
+    return KILN_OK;
+}
+
 int kiln_dit_step_cache_create(float threshold, kiln_dit_step_cache** out) {
     if (!out) return fail(KILN_EINVAL, "step_cache_create: null argument");
     return guarded([&] {

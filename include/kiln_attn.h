@@ -101,8 +101,11 @@ int kiln_attn_fwd_f16out(uint16_t* out, int ldo, const float* q, int ldq, const 
  * counterpart in the reference. Its scratch (fp16 K/V tiles, key-split partials) is a fixed device array of
  * kiln_attn_noalloc_scratch_bytes() (64 MiB) per device, held until the process ends; a call whose K/V tiles
  * (kiln_kv_prepped_bytes(Tk, H)) exceed it returns KILN_ENOMEM. It calls no hipMalloc/hipFree and never
- * synchronizes. Every call on one device shares that device's scratch: calls that overlap on one GPU (e.g. on
- * two streams) race. */
+ * synchronizes the host. Every call on one device shares that device's scratch, so eager calls are ordered on it:
+ * a call on another stream than the device's previous call first makes its stream wait for that call (one event
+ * per device, created at the first call; calls from several host threads are serialized). Calls under HIP graph
+ * capture skip that ordering: a replayed graph and calls on other streams must not overlap on one GPU (they would
+ * race on the scratch). */
 int kiln_attn_fwd_f16out_noalloc(uint16_t* out, int ldo, const float* q, int ldq, const float* k, int ldk,
                                  const float* v, int ldv, int Tq, int Tk, int H, int Dh, int npad,
                                  kiln_stream_t stream);

@@ -19,23 +19,35 @@ constexpr size_t SCRATCH_BYTES = (size_t)64 << 20;
 __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
 
 constexpr int MAX_DEVICES = 64;
-std::mutex g_mu;
-void* g_scratch[MAX_DEVICES] = {};
+std::mutex g_mu;  // held for a whole call: calls from several host threads reach the device one after another
 
-// the current device's scratch address, resolved on its first call on that device
-int scratch_of_current_device(void** out) {
+// Per device: the scratch address, and the stream and completion event of the last eager call. A call on another
+// stream than the last one first makes its stream wait for that event, so two streams never use the scratch at
+// once (calls on one stream are ordered by the stream itself and pay nothing).
+struct DeviceState {
+    void* scratch = nullptr;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool pending = false;  // `done` was recorded after the last eager call
+};
+DeviceState g_dev[MAX_DEVICES];
+
+// the current device's state, its scratch address and event set up on its first call on that device
+int state_of_current_device(DeviceState** out) {
     int dev = 0;
     if (int r = current_device(&dev)) return r;
     if (dev < 0 || dev >= MAX_DEVICES) return fail(KILN_EUNSUPPORTED, "device %d beyond %d", dev, MAX_DEVICES);
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (!g_scratch[dev]) {
+    DeviceState& st = g_dev[dev];
+    if (!st.scratch) {
         void* p = nullptr;
         hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(scratch)");
         if (!p) return fail(KILN_EHIP, "hipGetSymbolAddress(scratch) returned null");
-        g_scratch[dev] = p;
+        e = hipEventCreateWithFlags(&st.done, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_check(e, "hipEventCreateWithFlags");
+        st.scratch = p;
     }
-    *out = g_scratch[dev];
+    *out = &st;
     return KILN_OK;
 }
 
@@ -60,12 +72,27 @@ int kiln_attn_fwd_f16out_noalloc(uint16_t* out, int ldo, const float* q, int ldq
     if (need > SCRATCH_BYTES)
         return fail(KILN_ENOMEM, "attention16 (no-alloc): the prepared K/V of Tk=%d x H=%d take %zu bytes, above the "
                     "%zu-byte scratch", Tk, H, need, SCRATCH_BYTES);
-    void* ws = nullptr;
-    if ((r = scratch_of_current_device(&ws))) return r;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState* st = nullptr;
+    if ((r = state_of_current_device(&st))) return r;
+    const hipStream_t s = (hipStream_t)stream;
+    // Under graph capture the ordering against other streams is the caller's (a captured wait on an event of an
+    // eager call would tie the graph to that call): the guard covers eager calls only.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipError_t e = hipStreamIsCapturing(s, &cs); e != hipSuccess) return hip_check(e, "hipStreamIsCapturing");
+    const bool eager = cs == hipStreamCaptureStatusNone;
+    if (eager && st->pending && st->last != s) {
+        if (hipError_t e = hipStreamWaitEvent(s, st->done, 0); e != hipSuccess) return hip_check(e, "hipStreamWaitEvent");
+    }
     // Every scratch byte the kernels read is written earlier in the same call (prepared K/V, then the partials
     // of a key split), so nothing is cleared. The key split is taken only when its partials fit behind the K/V.
-    return flash_self(out, DT::F16, ldo, 0, q, ldq, 0, k, ldk, 0, v, ldv, 0, DT::F32, 1, Tq, Tk, H, npad, nullptr,
-                      nullptr, 0.f, nullptr, nullptr, ws, SCRATCH_BYTES, (hipStream_t)stream);
+    r = flash_self(out, DT::F16, ldo, 0, q, ldq, 0, k, ldk, 0, v, ldv, 0, DT::F32, 1, Tq, Tk, H, npad, nullptr, nullptr,
+                   0.f, nullptr, nullptr, st->scratch, SCRATCH_BYTES, s);
+    if (r || !eager) return r;
+    if (hipError_t e = hipEventRecord(st->done, s); e != hipSuccess) return hip_check(e, "hipEventRecord");
+    st->last = s;
+    st->pending = true;
+    return KILN_OK;
 }
 
 }  // extern "C"

@@ -49,3 +49,33 @@ def test_noalloc_rejects_beyond_scratch(gpu):
     out = torch.empty(8, H * D, dtype=torch.float16, device=DEV)
     assert _call(f, out, q, kv, kv, 8, Tk, 0) == kiln_amd.KILN_ENOMEM
     assert b"scratch" in gpu.kiln_attn_last_error()
+
+
+def test_noalloc_orders_calls_on_two_streams(gpu):
+    """Two streams alternate calls on the shared scratch without any host synchronization in between: the entry
+    point makes each call wait for the previous call on the other stream, so every output equals the allocating
+    entry point's (a long call is followed at once by a short one on the other stream)."""
+    f = _fn(gpu)
+    shapes = [(4096, 4096, 0), (200, 300, 3), (2048, 3000, 0), (64, 4000, 0)]
+    ins, refs = [], []
+    for n, (Tq, Tk, npad) in enumerate(shapes):
+        g = torch.Generator().manual_seed(300 + n)
+        q, k, v = (torch.randn(T, H * D, generator=g).to(DEV) for T in (Tq, Tk, Tk))
+        ref = torch.empty(Tq, H * D, dtype=torch.float16, device=DEV)
+        kiln_amd.attention16(ref, q, k, v, Tq, Tk, H, npad=npad)
+        ins.append((q, k, v))
+        refs.append(ref)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.full((T, H * D), float("nan"), dtype=torch.float16, device=DEV) for T, _, _ in shapes]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for n, (Tq, Tk, npad) in enumerate(shapes):
+            s = streams[n % 2]
+            print(f"[noalloc] two streams: rep {rep} call {n} Tq={Tq} Tk={Tk}", flush=True)
+            with torch.cuda.stream(s):
+                q, k, v = ins[n]
+                assert _call(f, outs[n], q, k, v, Tq, Tk, npad) == 0, gpu.kiln_attn_last_error().decode()
+        torch.cuda.synchronize()
+        for n in range(len(shapes)):
+            assert torch.equal(outs[n], refs[n]), f"rep {rep} call {n}: output differs from the allocating path"

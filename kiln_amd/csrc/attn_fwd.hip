@@ -42,6 +42,7 @@ struct AttnParams {
     AttnJob job[MAX_JOBS];
     int njobs, Tq, H, ldq, ldo, qtiles, total, per;
     int ksplit;   // key ranges per (query tile, head, job): > 1 writes partial (m, l, O) for k_attn_merge
+    int chain;    // context chain: a unit is a (query tile, head) and runs every job's keys in turn
     float* part;  // partials: [unit][ksplit] x (O [128 rows][128] fp32, then (m, l) per row)
     int store_pairs;  // ldo or an output base not 8/16-byte aligned: store element pairs
     int store_rows;   // ldo and every output base 16-byte aligned: output rows staged through LDS
@@ -318,12 +319,20 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
     static_assert(NWT == 4 || NWT == 8, "4 or 8 waves");
     constexpr int KNS = NWT == 8 ? NS8 : NS;               // ring stages (half tile j in stage j % KNS)
     static_assert(KNS == 4 || KNS == 8, "a power of two: stage = j & (KNS - 1)");
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane_in = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 4;  // 16-lane row of the wave: keys 4g..4g+3 of a key block, dims 8g.. of a d chunk
+    const int g_in = lane_in >> 4;  // 16-lane row of the wave: keys 4g..4g+3 of a key block, dims 8g.. of a d chunk
     Work W;
     if (!decode_work(p, W)) return;
-    const AttnJob J = p.job[W.jb];
+    half8 qreg[2][4];        // the Q tile (B operands); a context chain keeps it for consecutive jobs of one Q
+    const void* qcur = nullptr;
+    for (int jb = W.jb;; jb++) {  // the unit's job, or in a context chain each job in turn
+    if (jb != W.jb) __syncthreads();  // the previous job's output staging reads of the ring are done
+    // per-lane indices enter each job through an empty asm: otherwise the compiler hoists the job's lane-dependent
+    // addresses out of the job loop and keeps them live across the key loop
+    int lane = lane_in, g = g_in;
+    asm volatile("" : "+v"(lane), "+v"(g));
+    const AttnJob J = p.job[jb];
 
     const int Tk = J.Tk;
     const int nhall = (Tk + 31) / 32;  // half tiles holding real keys
@@ -371,13 +380,15 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
     __builtin_amdgcn_sched_barrier(0);
     int row[2];
     bool qin[2];
-    half8 qreg[2][4];
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
         row[qb] = W.qt * KBM + wv * 32 + 16 * qb + (lane & 15);
         qin[qb] = row[qb] < p.Tq;
     }
-    load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, g, qreg);
+    if (J.q != qcur) {
+        load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, g, qreg);
+        qcur = J.q;
+    }
 #pragma unroll
     for (int i = 3; i < KNS - 1; i++) dma(min(i, nh - 1), i);
     KILN_WAIT_VMCNT((KNS - 3) * KDMA);
@@ -582,7 +593,8 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
 #pragma unroll
         for (int qb = 0; qb < 2; qb++)
             epilogue_rows<OutT>(p, J, W.qt * KBM + wv * 32 + 16 * qb, W.h, g, lane, m[qb], l[qb], o[qb], stg);
-        return;
+        if (!p.chain || jb + 1 >= p.njobs) return;
+        continue;
     }
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
@@ -599,6 +611,8 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
             epilogue<OutT>(p, J, row[qb], qin[qb], W.h, g, m[qb], l[qb], o[qb]);
         }
     }
+    if (!p.chain || jb + 1 >= p.njobs) return;
+    }  // jobs
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -845,6 +859,9 @@ static hipError_t launch_sel(AttnParams p, int Tq, int units, hipStream_t s) {
     const int cus = resident_slots() / 2;
     bool longk = true;
     for (int i = 0; i < p.njobs; i++) longk &= p.job[i].Tk >= 2048;
+    // context chains run 4-wave units: at config 5's cross-attention (432 units of three 512-key contexts) 8-wave
+    // units (224 on 256 CUs) measured 62.1 against 58.1 us
+    if (p.chain) return launch_nw<InT, OutT, QN, RP, 4>(p, Tq, units, s);
     if (p.ksplit <= 1 && cus > 0 && (t8 % cus == 0 || (longk && t8 >= cus)))
         return launch_nw<InT, OutT, QN, RP, 8>(p, Tq, units, s);
     hipError_t e = launch_nw<InT, OutT, QN, RP, 4>(p, Tq, units, s);
@@ -881,10 +898,14 @@ hipError_t launch_attn_fwd(const AttnLaunch& a, hipStream_t s) {
     p.qscale = a.q_prescaled ? 1.0f : LOG2E / sqrtf((float)HD);
     p.rcos = a.rcos;
     p.rsin = a.rsin;
-    p.ksplit = a.part && a.ksplit > 1 ? a.ksplit : 1;
+    p.ksplit = a.part && a.ksplit > 1 && !a.chain ? a.ksplit : 1;
     p.part = a.part;
+    // context chains only where the per-context units take more than one round of the resident 4-wave slots
+    // (config 5's cross-attention: 1296 units, 2.53 rounds); below that a chain only empties slots (config 3:
+    // 384 per-context units, 192 chained: 27.7 -> 31.8 us)
+    p.chain = a.chain && a.njobs > 1 && (long)((a.Tq + BM - 1) / BM) * a.H * a.njobs > resident_slots();
     const bool qn = a.qw != nullptr, rp = a.rcos != nullptr;
-    const int units = a.H * a.njobs;
+    const int units = a.H * (p.chain ? 1 : a.njobs);
     if (a.Tq <= 0 || units <= 0) return hipSuccess;
     if (a.in == DT::F16) {
         if (a.out == DT::F16) return dispatch_attn<_Float16, _Float16>(p, units, qn, rp, s);

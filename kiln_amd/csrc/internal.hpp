@@ -32,6 +32,8 @@ struct AttnLaunch {
     int ksplit;          // > 1: split every unit's keys into ksplit ranges (partials in `part`, then a merge)
     float* part;         // attn_split_bytes(ksplit, njobs, Tq, H) bytes of device scratch
     bool q_prescaled;    // fp16 Q already holds q * log2(e)/sqrt(128) (no norm, no RoPE): scale 1
+    bool chain;          // context chain: one unit per (query tile, head) runs the jobs in order (jobs sharing a Q
+                         // pointer next to each other keep the Q tile in registers); no key split
 };
 
 // Key ranges per unit for a launch of njobs x H heads x Tq queries against Tk keys: > 1 only when the grid

@@ -311,7 +311,9 @@ static_assert(NS == 4, "ring: tiles j-1 (refilled), j, j+1 and j+2 (read this it
 // NWT waves per workgroup: 4 (two workgroups per CU, a 4-stage ring each) or 8 (one workgroup per CU, 256 query
 // rows sharing one 8-stage ring: half the K/V DMA, L2 reads and LDS writes per flop, which the power-limited
 // chip turns into clock).
-template <typename InT, typename OutT, bool QNORM, bool ROPE, int NWT>
+// CHAIN: a context chain (one unit per query tile and head, every job in turn); a separate instantiation, so
+// the one-job kernels compile exactly as without the job loop (the loop costs them ~1.5%).
+template <typename InT, typename OutT, bool QNORM, bool ROPE, int NWT, bool CHAIN>
 __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams p) {  // 2nd: workgroups per CU
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];  // NS x 16 KB
     constexpr int KBM = NWT * 32;                          // query rows of the workgroup
@@ -324,14 +326,10 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
     const int g_in = lane_in >> 4;  // 16-lane row of the wave: keys 4g..4g+3 of a key block, dims 8g.. of a d chunk
     Work W;
     if (!decode_work(p, W)) return;
-    half8 qreg[2][4];        // the Q tile (B operands); a context chain keeps it for consecutive jobs of one Q
-    const void* qcur = nullptr;
-    for (int jb = W.jb;; jb++) {  // the unit's job, or in a context chain each job in turn
-    if (jb != W.jb) __syncthreads();  // the previous job's output staging reads of the ring are done
-    // per-lane indices enter each job through an empty asm: otherwise the compiler hoists the job's lane-dependent
-    // addresses out of the job loop and keeps them live across the key loop
-    int lane = lane_in, g = g_in;
-    asm volatile("" : "+v"(lane), "+v"(g));
+    half8 qreg[2][4];  // the Q tile (B operands); a context chain keeps it for consecutive jobs of one Q
+    // one job of the unit: the keys of p.job[jb] for this query tile and head, with its epilogue; qload: load the
+    // Q tile (a chain skips it when the job shares the previous job's queries)
+    auto run_job = [&](int jb, int lane, int g, bool qload) {
     const AttnJob J = p.job[jb];
 
     const int Tk = J.Tk;
@@ -385,10 +383,7 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
         row[qb] = W.qt * KBM + wv * 32 + 16 * qb + (lane & 15);
         qin[qb] = row[qb] < p.Tq;
     }
-    if (J.q != qcur) {
-        load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, g, qreg);
-        qcur = J.q;
-    }
+    if (qload) load_q<InT, QNORM, ROPE>(p, J.q, row, qin, W.h, g, qreg);
 #pragma unroll
     for (int i = 3; i < KNS - 1; i++) dma(min(i, nh - 1), i);
     KILN_WAIT_VMCNT((KNS - 3) * KDMA);
@@ -593,8 +588,7 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
 #pragma unroll
         for (int qb = 0; qb < 2; qb++)
             epilogue_rows<OutT>(p, J, W.qt * KBM + wv * 32 + 16 * qb, W.h, g, lane, m[qb], l[qb], o[qb], stg);
-        if (!p.chain || jb + 1 >= p.njobs) return;
-        continue;
+        return;
     }
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
@@ -611,8 +605,22 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
             epilogue<OutT>(p, J, row[qb], qin[qb], W.h, g, m[qb], l[qb], o[qb]);
         }
     }
-    if (!p.chain || jb + 1 >= p.njobs) return;
-    }  // jobs
+    };  // run_job
+
+    if constexpr (!CHAIN) {
+        run_job(W.jb, lane_in, g_in, true);
+    } else {
+        const void* qcur = nullptr;
+        for (int jb = 0; jb < p.njobs; jb++) {
+            if (jb) __syncthreads();  // the previous job's output staging reads of the ring are done
+            // per-lane indices enter each job through an empty asm: otherwise the compiler hoists the job's
+            // lane-dependent addresses out of the job loop and keeps them live across the key loop
+            int lane = lane_in, g = g_in;
+            asm volatile("" : "+v"(lane), "+v"(g));
+            run_job(jb, lane, g, p.job[jb].q != qcur);
+            qcur = p.job[jb].q;
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -836,14 +844,14 @@ size_t attn_split_bytes(int ksplit, int njobs, int Tq, int H) {
     if (ksplit <= 1) return 0;
     return (size_t)((Tq + BM - 1) / BM) * H * njobs * ksplit * PART_FLOATS * sizeof(float);
 }
-template <typename InT, typename OutT, bool QN, bool RP, int NWT>
+template <typename InT, typename OutT, bool QN, bool RP, int NWT, bool CHAIN = false>
 static hipError_t launch_nw(AttnParams& p, int Tq, int units, hipStream_t s) {
     constexpr int KBM = NWT * 32;
     p.qtiles = (Tq + KBM - 1) / KBM;
     p.total = p.qtiles * units * p.ksplit;
     const int nb = (p.total + 7) / 8 * 8;
     p.per = nb / 8;
-    auto kern = k_attn_fwd<InT, OutT, QN, RP, NWT>;
+    auto kern = k_attn_fwd<InT, OutT, QN, RP, NWT, CHAIN>;
     // the ring, or the output staging of 16 rows per wave if that is larger (8 waves, fp32 output)
     const size_t lds = std::max((size_t)(NWT == 8 ? NS8 : NS) * HT_H * sizeof(_Float16), (size_t)NWT * 16 * ORS<OutT> * sizeof(OutT));
     hipLaunchKernelGGL(kern, dim3(nb), dim3(NWT * 64), lds, s, p);
@@ -861,7 +869,7 @@ static hipError_t launch_sel(AttnParams p, int Tq, int units, hipStream_t s) {
     for (int i = 0; i < p.njobs; i++) longk &= p.job[i].Tk >= 2048;
     // context chains run 4-wave units: at config 5's cross-attention (432 units of three 512-key contexts) 8-wave
     // units (224 on 256 CUs) measured 62.1 against 58.1 us
-    if (p.chain) return launch_nw<InT, OutT, QN, RP, 4>(p, Tq, units, s);
+    if (p.chain) return launch_nw<InT, OutT, QN, RP, 4, true>(p, Tq, units, s);
     if (p.ksplit <= 1 && cus > 0 && (t8 % cus == 0 || (longk && t8 >= cus)))
         return launch_nw<InT, OutT, QN, RP, 8>(p, Tq, units, s);
     hipError_t e = launch_nw<InT, OutT, QN, RP, 4>(p, Tq, units, s);

@@ -9,6 +9,10 @@ a reference run. All calls go through the C ABI.
   visits the keys in another order), to fp16 output rounding.
 * Determinism: two identical calls give bit-identical outputs.
 * CFG batching: the batched fused call equals one call per batch item, bit for bit.
+* One key (Tk = 1): every softmax weight is exactly 1, so every query row's output is that key's V row, bit for bit
+  (fp16 V through an fp32 accumulator back to fp16).
+* Identical keys: every score of a row is the same, every weight exactly 1 after the max shift, so the output is
+  the mean of the V rows (the row sum counts the keys exactly), to fp16 output rounding.
 """
 import numpy as np
 import pytest
@@ -130,3 +134,35 @@ def test_cross_attention_nag_full_size_neutral(gpu):
     err = (nag[:T].float() - plain[:T].float()).abs().max().item()
     print(f"[parity] neutral NAG on item 0: max diff {err:.3e}", flush=True)
     assert err <= 1e-3
+
+
+def test_single_key_returns_its_value_row(gpu):
+    B, Tq = 2, 4096
+    print(f"[case] Tk=1, fp16-in batched attention B={B} Tq={Tq}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(51)
+    q = torch.randn(B * Tq, H * D, generator=g, device=DEV).half()
+    k = torch.randn(B, H * D, generator=g, device=DEV).half()
+    v = torch.randn(B, H * D, generator=g, device=DEV).half()
+    o = torch.empty_like(q)
+    kiln_amd.attn_f16in(o, q, k, v, B, Tq, 1, H)
+    torch.cuda.synchronize()
+    for b in range(B):
+        assert torch.equal(o[b * Tq:(b + 1) * Tq], v[b:b + 1].expand(Tq, -1)), f"item {b}: output is not V's one row"
+    print("[parity] Tk=1: every output row equals the key's V row", flush=True)
+
+
+@pytest.mark.parametrize("Tk", [4096, 1000])  # whole 64-key tiles, and a ragged last half tile
+def test_identical_keys_give_mean_value(gpu, Tk):
+    Tq = 2048
+    print(f"[case] identical keys, fp16-in attention Tq={Tq} Tk={Tk}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(61)
+    q = torch.randn(Tq, H * D, generator=g, device=DEV).half()
+    k = torch.randn(1, H * D, generator=g, device=DEV).half().expand(Tk, -1).contiguous()
+    v = torch.randn(Tk, H * D, generator=g, device=DEV).half()
+    o = torch.empty_like(q)
+    kiln_amd.attn_f16in(o, q, k, v, 1, Tq, Tk, H)
+    torch.cuda.synchronize()
+    mean = v.double().mean(0, keepdim=True).expand(Tq, -1)
+    err = (o.double() - mean).abs().max().item()
+    print(f"[parity] identical keys: max |out - mean(V)| = {err:.3e}", flush=True)
+    assert err <= 2e-4  # |mean| ~ 0.02-0.1: fp16 rounding of the output (<= 2^-14) and fp32 sums of Tk terms

@@ -256,12 +256,14 @@ __device__ __forceinline__ void qkv_epilogue(const GemmParams& p, floatx4 (&acc)
     }
 }
 
-// LATE (prepared weights): in steady steps waves 4-7 issue their refill after the third activation block's MFMAs
-// instead of right after the barrier. Waves w and w + 4 share a SIMD; with both refills issued together, the
-// DMA issue stalls of the two waves coincide and the matrix core idles through them. Measured on the DiT shapes
-// (A/B on one box): MLP down -3.3%, the block's four GEMMs -1.7%; the same split slows plain-weight launches
-// (whose W rows arrive as 64-byte row pieces) by ~2%, which keep the refill after the barrier.
-constexpr int LATE_MB = 3;
+// LATE (prepared weights): in steady steps the refill DMA leaves the barrier's shadow and the two waves of a SIMD
+// issue it at different points of the MFMA stream: waves 0-3 after the first activation block's MFMAs, waves 4-7
+// after the fourth. Waves w and w + 4 share a SIMD; with both refills issued together right after the barrier,
+// the DMA issue stalls of the two waves coincide and the matrix core idles through them. Measured on the DiT
+// shapes (A/B on one box): the block's four GEMMs -1.4% with waves 4-7 moved, -1.0 to -1.9% more with waves 0-3
+// moved as well; the split slows plain-weight launches (whose W rows arrive as 64-byte row pieces) by ~2%, which
+// keep the refill after the barrier.
+constexpr int EARLY_MB = 1, LATE_MB = 3;
 template <int EPI, int MB, bool LATE>
 __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
     using TL = Tile<MB>;
@@ -402,8 +404,8 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage kt are complete
         __builtin_amdgcn_s_barrier();
-        const bool late = LATE && STEADY && wv >= 4;
-        if (!late && (STEADY || kt + GNS < KTT)) dma(kt + GNS, kt % GNS);
+        const bool split = LATE && STEADY;  // the refill moves into the MFMA stream (position by wave)
+        if (!split && (STEADY || kt + GNS < KTT)) dma(kt + GNS, kt % GNS);
         __builtin_amdgcn_sched_barrier(0);
         const int nst = (kt + 1) % GNS;
         const bool more = STEADY || ahead >= 1;
@@ -416,7 +418,7 @@ __global__ __launch_bounds__(GTHR, 1) void k_gemm16(const GemmParams p) {
 #pragma unroll
             for (int nb = 0; nb < NBW; nb++) acc[nb][mb] = mfma16(cw[nb], fa[mb], acc[nb][mb]);
             if (more) fa[mb] = afrag(nst, mb);
-            if (late && mb == LATE_MB) {
+            if (split && mb == (wv >= 4 ? LATE_MB : EARLY_MB)) {
                 __builtin_amdgcn_sched_barrier(0);
                 dma(kt + GNS, kt % GNS);
                 __builtin_amdgcn_sched_barrier(0);

@@ -299,7 +299,7 @@ __device__ __forceinline__ void epilogue_rows(const AttnParams& p, const AttnJob
 //   K_{j+1} chunks 2-3, V_j[db 0-3] reads | QK_{j+1} MFMAs interleaved with exp/cvt of S_j |
 //   wait tile j+2, barrier | DMA tile j+NS-1 into the stage of tile j-1 | K_{j+2} chunks 0-1, V_j[db 4-7] reads |
 //   PV_j and row-sum MFMAs interleaved with max(S_{j+1})
-// (one-job 4-wave workgroups issue the DMA at the end of the step instead)
+// (one-job 4-wave workgroups issue the DMA between the two halves of the PV MFMAs instead)
 // Every read of a stage completes before the barrier that precedes its refill.
 // ------------------------------------------------------------------------------------------------
 // a scheduling fence: keeps the phases of a step in the order written and bounds the live registers
@@ -466,11 +466,11 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
     // Tile j+2 landed in every wave; every wave is done with tile j-1, whose stage is refilled. Only tiles
     // j+3 .. j+KNS-2 may be in flight; the peeled masking step (whose register spills, if any, are vector memory
     // operations too) waits for everything.
-    // One-job 4-wave workgroups issue the plain steps' refill at the end of the step instead of right after the
-    // barrier, where it delays the K_{j+2} / V_j operand reads that the PV MFMAs wait for (config 2: -1.2%; the
-    // two workgroups of a CU run in step with each other, and their issue stalls add up there; key-split launches
-    // of short ranges lose ~1.5% with it). Context chains keep it after the barrier (their short jobs measured +5%
-    // with it), and so do 8-wave workgroups (no change).
+    // One-job 4-wave workgroups issue the plain steps' refill between the two halves of the PV MFMAs instead of
+    // right after the barrier, where it delays the K_{j+2} / V_j operand reads that the PV MFMAs wait for (the two
+    // workgroups of a CU run in step with each other, and their issue stalls add up there): config 2 kernel
+    // -1.5%, config 3 -1%; at the end of the step: config 2 -1.2%. Context chains keep it after the barrier
+    // (their short jobs measured +5% with it at the end of the step), and so do 8-wave workgroups (no change).
     constexpr bool REFILL_LATE = NWT == 4 && !CHAIN;
     auto sync_refill = [&](auto maskn_tag, int j) {
         if constexpr (decltype(maskn_tag)::value) KILN_WAIT_VMCNT(0);
@@ -530,6 +530,11 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
         for (int db = 0; db < 4; db++)
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) o[qb][db] = mfma16(va[db], pb[qb], o[qb][db]);
+        if constexpr (REFILL_LATE && !MASKN) {
+            KILN_FENCE();
+            dma(min(j + KNS - 1, nh - 1), stage(j + KNS - 1));
+            KILN_FENCE();
+        }
 #pragma unroll
         for (int db = 0; db < 4; db++)
 #pragma unroll
@@ -539,7 +544,6 @@ __global__ __launch_bounds__(NWT * 64, 8 / NWT) void k_attn_fwd(const AttnParams
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) mx[qb] = max8(sn[0][qb], sn[1][qb]);
         KILN_FENCE();
-        if constexpr (REFILL_LATE && !MASKN) dma(min(j + KNS - 1, nh - 1), stage(j + KNS - 1));
     };
 
     using True = std::true_type;

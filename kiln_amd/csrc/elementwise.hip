@@ -87,21 +87,30 @@ __device__ __forceinline__ void st4(_Float16* p, floatx4 v) {
     *reinterpret_cast<half4*>(p) = h;
 }
 
+// A wave normalizes LN_RPW consecutive rows with the modulation vectors loaded once (per row they would be twice
+// the row's own bytes in L2 reads; 6912 x 2048 fp16 out: 15.4 -> 14.4 us against one row per wave).
+constexpr int LN_RPW = 4;
 template <typename OutT, int NC>
 __global__ __launch_bounds__(256) void k_layernorm_mod_rows(OutT* y, const float* x, const float* scale,
                                                             const float* shift, int rows, int dim, float eps) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * LN_RPW;
+    if (row0 >= rows) return;
+    const int nc = dim / 4;
+    floatx4 v[NC], sc[NC], sh[NC];  // a row and the modulation; the row's loads issued before its reductions
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        const int c = min(lane + 64 * k, nc - 1);
+        sc[k] = *reinterpret_cast<const floatx4*>(scale + 4 * c);
+        sh[k] = *reinterpret_cast<const floatx4*>(shift + 4 * c);
+    }
+    for (int row = row0; row < min(row0 + LN_RPW, rows); row++) {
     const float* xr = x + (size_t)row * dim;
     OutT* yr = y + (size_t)row * dim;
-    const int nc = dim / 4;
-    floatx4 v[NC], sc[NC], sh[NC];  // the row and its modulation, all loads issued before the reductions
 #pragma unroll
     for (int k = 0; k < NC; k++) {
         const int c = min(lane + 64 * k, nc - 1);
         v[k] = *reinterpret_cast<const floatx4*>(xr + 4 * c);
-        sc[k] = *reinterpret_cast<const floatx4*>(scale + 4 * c);
-        sh[k] = *reinterpret_cast<const floatx4*>(shift + 4 * c);
     }
     float s = 0.f;
 #pragma unroll
@@ -128,6 +137,7 @@ __global__ __launch_bounds__(256) void k_layernorm_mod_rows(OutT* y, const float
             st4(yr + 4 * c, o);
         }
     }
+    }
 }
 
 // any dim / alignment: three passes over the row (the second and third hit the cache)
@@ -153,12 +163,12 @@ __global__ __launch_bounds__(256) void k_layernorm_mod_any(OutT* y, const float*
 template <typename OutT>
 static hipError_t layernorm_mod_sel(OutT* y, const float* x, const float* scale, const float* shift, int rows, int dim,
                                     float eps, bool vec, hipStream_t s) {
-    const dim3 grid((rows + 3) / 4), block(256);
+    const dim3 grid((rows + 3) / 4), block(256), grid_rows((rows + 4 * LN_RPW - 1) / (4 * LN_RPW));
     const int nc = dim / 4;
-    if (vec && nc <= 64 * 2) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 2>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
-    else if (vec && nc <= 64 * 4) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 4>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
-    else if (vec && nc <= 64 * 8) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 8>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
-    else if (vec && nc <= 64 * 16) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 16>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    if (vec && nc <= 64 * 2) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 2>), grid_rows, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    else if (vec && nc <= 64 * 4) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 4>), grid_rows, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    else if (vec && nc <= 64 * 8) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 8>), grid_rows, block, 0, s, y, x, scale, shift, rows, dim, eps);
+    else if (vec && nc <= 64 * 16) hipLaunchKernelGGL((k_layernorm_mod_rows<OutT, 16>), grid_rows, block, 0, s, y, x, scale, shift, rows, dim, eps);
     else hipLaunchKernelGGL((k_layernorm_mod_any<OutT>), grid, block, 0, s, y, x, scale, shift, rows, dim, eps);
     return hipGetLastError();
 }

@@ -219,7 +219,7 @@ def test_f16_rounding_matches_numpy():
     np.testing.assert_array_equal(oracle.to_f16_bits(x), x.astype(np.float16).view(np.uint16))
 
 
-# ---- modulated LayerNorm and gated residual of the DiT block (SURVEY 8(f) next rows) ----
+# ---- modulated LayerNorm and gated residual of the DiT block ----
 def test_layernorm_mod_matches_torch_float64():
     """oracle.layernorm_mod against an independent float64 statement: torch layer_norm without affine,
     then * (1 + scale) + shift (engine/src/kernels.cu:678-697)."""
